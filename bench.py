@@ -1,0 +1,267 @@
+"""Benchmark: Qwen3-Omni-thinker-shaped paged decode on one MI355X (BASELINE config c3).
+
+One step = one pass of the attention hot path for one layer over the whole
+ragged batch, through the drop-in surface M*'s engine calls:
+
+  BatchedCacheManager.plan_attention([1]*B)  host FIFO allocation of new pages,
+                                             block-table delta, mi_pack, mi_decode_plan
+  BatchedCacheManager.run_attention(q, k, v) mi_kv_append, decode kernel, merge kernel
+  advance_seq_lens()
+
+Inputs are resident in HBM before timing: a 262144-page bf16 KV pool
+(8.6 GB, random N(0,1)), B=256 requests with log-uniform [512, 32768]
+contexts on randomly permuted pages (seed 2).  ``value`` = decode tokens/s
+= B / wall-clock ms per step.  ``roofline`` reports the decode kernel alone:
+algorithmic bytes of one launch (KV read of every token + q read + o write +
+index arrays; split-KV partials excluded) over its average duration from HIP
+events on the launch stream.  ``cpu_baseline`` times the CPU restatement
+(``oracle/``) on a bounded sample of the same requests on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+from mstar_amd import _lib  # noqa: E402
+from mstar_amd import synthetic as S  # noqa: E402
+from mstar_amd.cache_manager import BatchedCacheManager, WorkspaceBufferManager  # noqa: E402
+from mstar_amd.kv_store import KVCacheConfig, PagedAllocationManager  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged decode attn tokens/s + achieved HBM GB/s (% peak), 1 MI355X, B=256"
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def setup(spec_name: str, device: torch.device):
+    bt = S.make_batch(spec_name)
+    s = bt.spec
+    b = len(bt.kv_len)
+    cfg = KVCacheConfig(num_layers=1, num_kv_heads=s.num_kv_heads, head_dim=s.head_dim,
+                        max_seq_len=40960, max_num_pages=s.pool_pages, page_size=s.page_size,
+                        num_qo_heads=s.num_qo_heads)
+    kv = torch.empty(1, s.pool_pages, 2, s.page_size, s.num_kv_heads, s.head_dim, dtype=torch.bfloat16,
+                     device=device)
+    gen = torch.Generator(device=device).manual_seed(s.seed)
+    chunk = 1 << 14
+    for p0 in range(0, s.pool_pages, chunk):
+        kv[0, p0:p0 + chunk].normal_(generator=gen)
+    mgr = PagedAllocationManager(cfg, kv, device=device)
+    # Steady state: each request already holds its T-1 cached tokens on the
+    # drawn (random) pages; the allocator's free list holds the rest of the
+    # permutation, so new pages keep coming from random places.
+    used = set(bt.kv_indices.tolist())
+    perm_rest = [p for p in torch.randperm(s.pool_pages, generator=torch.Generator().manual_seed(s.seed + 100)).tolist()
+                 if p not in used]
+    mgr.page_allocator.free_pages.clear()
+    mgr.page_allocator.free_pages.extend(perm_rest)
+    rids = [f"req{i}" for i in range(b)]
+    for i, r in enumerate(rids):
+        mgr.add_request(r, ["main"])
+        st = mgr.get_state(r, "main")
+        st.page_indices = bt.kv_indices[bt.kv_indptr[i]:bt.kv_indptr[i + 1]].tolist()
+        st.seq_len = int(bt.kv_len[i]) - 1
+        st.position_id_start = st.seq_len
+    bufs = WorkspaceBufferManager(512 << 20, device)  # the reference's per-label workspace size
+    cm = BatchedCacheManager(rids, {r: "main" for r in rids}, kv, mgr, bufs, cfg, device)
+    g = torch.Generator().manual_seed(s.seed + 1)
+    q = torch.randn(b, s.num_qo_heads, s.head_dim, generator=g).to(torch.bfloat16).to(device)
+    k = torch.randn(b, s.num_kv_heads, s.head_dim, generator=g).to(torch.bfloat16).to(device)
+    v = torch.randn(b, s.num_kv_heads, s.head_dim, generator=g).to(torch.bfloat16).to(device)
+    return bt, cfg, kv, mgr, cm, rids, q, k, v
+
+
+def decode_bytes(seq_lens_after: np.ndarray, total_pages: int, s) -> int:
+    """Algorithmic HBM bytes of one decode-kernel launch (partials excluded)."""
+    b = len(seq_lens_after)
+    kv = int(seq_lens_after.sum()) * s.num_kv_heads * s.head_dim * 2 * 2
+    qo = b * s.num_qo_heads * s.head_dim * 2 * 2
+    idx = 4 * (total_pages + 3 * b)
+    return kv + qo + idx
+
+
+def step_once(cm, q, k, v, b, events=None):
+    cm.plan_attention([1] * b)
+    wrapper = cm._plan_states["main"].wrapper
+    layer = cm.kv_cache[0]
+    wrapper.set_kv_cache(layer, k, v)
+    if events is None:
+        out = wrapper.run(q, layer)
+    else:
+        out = _run_split(wrapper, q, layer, events)
+    cm.advance_seq_lens()
+    return out
+
+
+def _run_split(w, q, layer, events):
+    """wrapper.run() as its two C entry points, with HIP events around the decode kernel."""
+    desc = _lib.paged_kv_desc(layer)
+    out = torch.empty_like(q)
+    args = (q.data_ptr(), _lib.MI_BF16, q.stride(0), q.stride(1), desc, None, w._indptr.data_ptr(),
+            w._indices.data_ptr(), w._last.data_ptr(), w._n_req, w.num_qo_heads, 0, 1.0 / math.sqrt(w.head_dim),
+            w._workspace.data_ptr(), w._workspace.numel(), out.data_ptr(), out.stride(0), out.stride(1),
+            _lib.stream_ptr(q.device))
+    e0, e1 = events
+    e0.record()
+    _lib.check(_lib.lib().mi_decode_attend(*args), "mi_decode_attend")
+    e1.record()
+    _lib.check(_lib.lib().mi_decode_merge(*args), "mi_decode_merge")
+    return out
+
+
+def cpu_baseline(bt, kv_gpu, q, k, v, budget_s: float = 12.0):
+    """The CPU restatement (oracle/) on a sample of the batch: pack + append + fp32 attention."""
+    from oracle import attention as A
+    from oracle import packing as P
+
+    s = bt.spec
+    threads = min(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), 16)
+    torch.set_num_threads(threads)
+    nreq = 16
+    sub = S.truncate(bt, nreq)
+    pages = sub.kv_indices
+    uniq = np.unique(pages)
+    remap = {int(p): i for i, p in enumerate(uniq)}
+    cache = kv_gpu[0, torch.as_tensor(uniq, device=kv_gpu.device)].cpu()
+    idx = np.asarray([remap[int(p)] for p in pages], dtype=np.int32)
+    qc, kc, vc = q[:nreq].cpu(), k[:nreq].cpu(), v[:nreq].cpu()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        states, extra = [], []
+        for i in range(nreq):
+            pl = idx[sub.kv_indptr[i]:sub.kv_indptr[i + 1]].tolist()
+            cached = int(sub.kv_len[i]) - 1
+            keep = -(-cached // s.page_size)
+            states.append(P.ReqState(pages=pl[:keep], seq_len=cached))
+            extra += pl[keep:]  # a page the new token opens comes from the free list
+        pool = P.FifoPages(0)
+        pool.free.extend(extra)
+        packed = P.pack(states, [1] * nreq, pool, s.page_size)
+        loc = packed.kv_locations
+        A.append(cache, loc[:, 0], loc[:, 1], kc, vc)
+        A.paged_attention(qc, cache, None, packed.kv_indptr, packed.kv_indices, packed.last_page_len, causal=False)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 10 and time.perf_counter() > t_end:
+            break
+    med = float(np.median(times))
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": nreq / med,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"first {nreq} of the {len(bt.kv_len)} c3 requests ({int(sub.kv_len.sum())} KV tokens), "
+                   f"pack + append + fp32 paged attention, median of {len(times)} runs, "
+                   f"{threads} host threads, CPU: {model}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    _lib.lib()
+    _log(f"setup {args.config} ...")
+    bt, cfg, kv, mgr, cm, rids, q, k, v = setup(args.config, dev)
+    s = bt.spec
+    b = len(rids)
+    torch.cuda.synchronize()
+    _log(f"warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        step_once(cm, q, k, v, b)
+    torch.cuda.synchronize()
+
+    # timed region 1: the full hot path per step, wall clock
+    _log(f"timing {args.steps} steps")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step_once(cm, q, k, v, b)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+
+    # timed region 2: same steps, decode kernel bracketed by HIP events
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    bytes_per = []
+    for i in range(args.steps):
+        seq_after = np.array([cm._get_state(r).seq_len + 1 for r in rids])
+        step_once(cm, q, k, v, b, events=evs[i])
+        bytes_per.append(decode_bytes(seq_after, sum(len(cm._get_state(r).page_indices) for r in rids), s))
+    torch.cuda.synchronize()
+    dec_ms = np.array([a.elapsed_time(bb) for a, bb in evs])
+    dec_s = float(dec_ms.mean()) / 1e3
+    achieved = float(np.mean(bytes_per)) / dec_s / 1e9
+    kv_tokens = int(sum(cm._get_state(r).seq_len for r in rids))
+    res = {
+        "metric": METRIC,
+        "value": b / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{s.name}: Qwen3-Omni thinker decode, one layer-step of pack+plan+append+decode+merge",
+            "batch": b, "num_qo_heads": s.num_qo_heads, "num_kv_heads": s.num_kv_heads, "head_dim": s.head_dim,
+            "page_size": s.page_size, "context": "log-uniform [512, 32768]", "kv_pool_pages": s.pool_pages,
+            "kv_tokens_at_end": kv_tokens,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "kernel": "decode_kernel",
+            "kernel_us": dec_s * 1e6,
+            "algorithmic_bytes": int(np.mean(bytes_per)),
+        },
+    }
+    if not args.no_cpu_baseline:
+        _log("cpu baseline ...")
+        res["cpu_baseline"] = cpu_baseline(bt, kv, q, k, v)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,208 @@
+/*
+ * mstar_amd.h — C ABI of the MI355X (gfx950) ragged paged-attention library.
+ *
+ * This is the drop-in boundary for M*'s continuous-batch attention path:
+ * per-step batch packing, paged KV-cache append and paged attention.  Every
+ * entry point takes raw device pointers, explicit sizes and a hipStream_t
+ * (passed as void*), launches asynchronously on that stream, allocates no
+ * memory and returns an int status (MI_OK == 0, negative on error).  No C++
+ * exception crosses this boundary.  Buffers belong to the caller: the KV
+ * pool, the per-wrapper workspace, index tensors and outputs.
+ *
+ * Layout of one KV layer (M*'s "NHD" layout, kv_cache_engine.py:132-136):
+ *   [max_pages, 2 (K,V), page_size, num_kv_heads, head_dim]
+ * described by mi_paged_kv with explicit element strides.
+ *
+ * Threading: no global mutable state; plan and run of different workspaces
+ * may run concurrently on different streams.
+ */
+#ifndef MSTAR_AMD_H
+#define MSTAR_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element type codes */
+#define MI_BF16 0
+#define MI_F16 1
+#define MI_F32 2
+#define MI_FP8_E4M3 3 /* OCP e4m3fn (gfx950 native), max 448, per-head fp32 scales */
+
+/* status codes */
+#define MI_OK 0
+#define MI_ERR_INVALID (-1)     /* bad argument (null pointer, size, stride) */
+#define MI_ERR_UNSUPPORTED (-2) /* valid but not implemented (dtype, head_dim, page_size) */
+#define MI_ERR_WORKSPACE (-3)   /* workspace too small or not planned for this call */
+#define MI_ERR_LAUNCH (-4)      /* HIP launch error */
+
+#define MI_ABI_VERSION 1
+
+/* One layer of the paged KV cache. Strides are in elements. */
+typedef struct mi_paged_kv {
+  void* data;           /* element (page 0, K, slot 0, head 0, dim 0) */
+  int32_t dtype;        /* MI_BF16, MI_F16 or MI_FP8_E4M3 */
+  int32_t page_size;    /* tokens per page */
+  int32_t num_kv_heads;
+  int32_t head_dim;     /* 64, 128 or 256 */
+  int64_t max_pages;    /* pages in the pool; page ids outside [0, max_pages) are skipped by append */
+  int64_t page_stride;  /* between consecutive pages */
+  int64_t kv_stride;    /* from the K half of a page to its V half */
+  int64_t token_stride; /* between slots of a page */
+  int64_t head_stride;  /* between kv heads of a slot (head_dim elements must be contiguous) */
+  const float* k_scale; /* MI_FP8_E4M3 only: [num_kv_heads] dequantisation scales, else NULL */
+  const float* v_scale;
+} mi_paged_kv;
+
+/* Human-readable text for a status code (static storage). */
+const char* mi_status_string(int status);
+
+/* MI_ABI_VERSION of the loaded library. */
+int mi_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * P1 — per-step batch packing on the GPU.
+ * Replaces the Python packing loop of BatchedCacheManager._plan_attention_impl
+ * (mstar/engine/cache_manager.py:272-322).  Pages must already be allocated
+ * (host FIFO allocator, mstar/engine/kv_store.py:463-482) and present in the
+ * device block table.  For request r (batch order):
+ *   T_r             = seq_len[r] + new_len[r]
+ *   qo_indptr[r+1]  = qo_indptr[r] + new_len[r]
+ *   kv_indptr[r+1]  = kv_indptr[r] + num_pages[r]
+ *   kv_indices[kv_indptr[r] + p] = block_table[req_slot[r] * block_table_stride + p]
+ *   last_page_len[r]= T_r % page_size, or page_size when that is 0
+ *   kv_locations[r] = (last page of the request's list, last_page_len[r] - 1) when
+ *                     new_len[r] == 1 (cache_manager.py:293-294), (-1, -1) if the list
+ *                     is empty; only if kv_locations != NULL (int64 [batch, 2]); rows
+ *                     with new_len != 1 are left untouched
+ * grid_blocks: number of workgroups to launch (>= 1); every workgroup
+ * recomputes the two prefix sums, so no inter-block synchronisation is needed.
+ * ------------------------------------------------------------------------ */
+int mi_pack(const int32_t* req_slot, const int32_t* seq_len, const int32_t* new_len,
+            const int32_t* num_pages, int32_t batch, const int32_t* block_table,
+            int64_t block_table_stride, int32_t page_size, int32_t* qo_indptr,
+            int32_t* kv_indptr, int32_t* kv_indices, int32_t* last_page_len,
+            int64_t* kv_locations, int32_t grid_blocks, void* stream);
+
+/* Incremental device block-table update: block_table[slot[i]*stride + pos[i]] = page[i]
+ * for i < n.  Keeps the device copy of each request's page list in step with the
+ * host allocator (mstar/engine/kv_store.py:463-482) without re-sending whole lists. */
+int mi_block_table_update(int32_t* block_table, int64_t stride, const int32_t* slot,
+                          const int32_t* pos, const int32_t* page, int32_t n, void* stream);
+
+/* ------------------------------------------------------------------------
+ * P4 — decode plan: split-KV work partition built on the GPU.
+ * Replaces FlashInfer's BatchDecodeWithPagedKVCacheWrapper.plan as called from
+ * FlashInferDecodeWrapper.plan (mstar/utils/flashinfer_utils.py:369-453),
+ * including the write locations of flashinfer_utils.py:433-436.
+ * qo_indptr == NULL means one query token per request (decode); otherwise
+ * request r has qo_indptr[r+1]-qo_indptr[r] query tokens and
+ * (query tokens) * (num_qo_heads/num_kv_heads) must be <= 16 for every request.
+ * kv_locations (nullable, int64 [batch, 2]) receives
+ * (kv_indices[kv_indptr[r+1]-1], last_page_len[r]-1), or (-1, -1) when the
+ * request holds no page.
+ * mi_decode_workspace_bytes gives the recommended workspace size; a smaller
+ * workspace makes the plan use fewer, longer KV chunks (MI_ERR_WORKSPACE only
+ * when not even batch+1 chunks fit).  The plan is stored in the workspace and
+ * read by mi_decode_run, which must get the same workspace size.
+ * ------------------------------------------------------------------------ */
+int64_t mi_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                  int32_t head_dim);
+int mi_decode_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
+                   const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                   int32_t page_size, int32_t num_qo_heads, int32_t num_kv_heads,
+                   int32_t head_dim, int64_t* kv_locations, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * P6 — paged GQA decode attention (+ split-KV merge).
+ * Replaces FlashInferDecodeWrapper.run (mstar/utils/flashinfer_utils.py:455-465).
+ *   out[t, h, :] = softmax(sm_scale * q[t,h,:] . K_r[:, h / G, :]) V_r[:, h / G, :]
+ * over the request's kv_len = (npages-1)*page_size + last_page_len tokens
+ * (causal alignment to the end of the KV when a request has several query
+ * tokens and causal != 0).  q and out: [tokens, num_qo_heads, head_dim] with
+ * the given element strides (head_dim contiguous), dtype q_dtype (bf16/fp16).
+ * Requests without KV produce zeros.
+ * mi_decode_run = mi_decode_attend (one wavefront per (KV chunk, kv-head):
+ * finished rows of unsplit requests, partial (o, lse) of split ones) followed
+ * by mi_decode_merge (log-sum-exp merge of the partials); the two halves take
+ * the same arguments and may be called separately on the same stream.
+ * ------------------------------------------------------------------------ */
+int mi_decode_run(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                  const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                  const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                  int32_t num_qo_heads, int32_t causal, float sm_scale, void* workspace,
+                  int64_t workspace_bytes, void* out, int64_t out_stride_token,
+                  int64_t out_stride_head, void* stream);
+int mi_decode_attend(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                     const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                     const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                     int32_t num_qo_heads, int32_t causal, float sm_scale, void* workspace,
+                     int64_t workspace_bytes, void* out, int64_t out_stride_token,
+                     int64_t out_stride_head, void* stream);
+int mi_decode_merge(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                    const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                    const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                    int32_t num_qo_heads, int32_t causal, float sm_scale, void* workspace,
+                    int64_t workspace_bytes, void* out, int64_t out_stride_token,
+                    int64_t out_stride_head, void* stream);
+
+/* ------------------------------------------------------------------------
+ * P5 — paged KV append.
+ * Replaces FlashInferPrefillWrapper.set_kv_cache / FlashInferDecodeWrapper.set_kv_cache
+ * (mstar/utils/flashinfer_utils.py:271-288, 467-484):
+ *   cache[page[i], K, slot[i]] = k[i];  cache[page[i], V, slot[i]] = v[i]
+ * cast to the cache dtype (RNE; fp8: x * (1/scale) clamped to +-448, then RNE).
+ * page[i] = page_idx[i * idx_stride], slot[i] = slot_idx[i * idx_stride]
+ * (idx_stride 1 for token_to_page/token_to_cache, 2 for kv_cache_locations
+ * [B, 2] with slot_idx = page_idx + 1).  Tokens whose page id is outside
+ * [0, max_pages) or slot outside [0, page_size) are skipped.  When
+ * num_tokens_device != NULL only the first min(num_tokens, *num_tokens_device)
+ * tokens are written (graph-replay padding is dropped).
+ * k, v: [num_tokens, num_kv_heads, head_dim], element strides given, dtype src_dtype.
+ * ------------------------------------------------------------------------ */
+int mi_kv_append(const mi_paged_kv* kv, const void* k, const void* v, int32_t src_dtype,
+                 int64_t k_stride_token, int64_t k_stride_head, int64_t v_stride_token,
+                 int64_t v_stride_head, const int64_t* page_idx, const int64_t* slot_idx,
+                 int64_t idx_stride, int32_t num_tokens, const int32_t* num_tokens_device,
+                 void* stream);
+
+/* ------------------------------------------------------------------------
+ * P3 + P7 — ragged prefill plan and attention.
+ * mi_prefill_plan replaces FlashInferPrefillWrapper.plan
+ * (mstar/utils/flashinfer_utils.py:162-256): it writes the per-token page map
+ *   token_to_page[t]  = kv_indices[kv_indptr[r] + g / page_size]
+ *   token_to_cache[t] = g % page_size,  g = kv_len_r - qo_len_r + (t - qo_indptr[r])
+ * for t < qo_indptr[batch] (entries in [qo_indptr[batch], token_map_len) are set
+ * to 0, like the graph-mode tail fill of flashinfer_utils.py:251-253), and the
+ * work partition for mi_prefill_run into the workspace.  Requests whose
+ * qo_len * (num_qo_heads/num_kv_heads) <= 16 go to the split-KV decode kernel,
+ * longer ones to the MFMA prefill kernel.
+ * max_qo_tokens bounds qo_indptr[batch] (grid sizing without a host sync);
+ * mi_prefill_run must get the same batch, max_qo_tokens and workspace.
+ * mi_prefill_run replaces FlashInferPrefillWrapper.run (:258-269):
+ *   out[t, h] = softmax(sm_scale * q[t,h] . K_r^T) V_r over the request's keys
+ *   i <= kv_len - qo_len + j for query j (causal) or all kv_len keys.
+ * ------------------------------------------------------------------------ */
+int64_t mi_prefill_workspace_bytes(int32_t batch, int32_t max_qo_tokens, int32_t num_qo_heads,
+                                   int32_t num_kv_heads, int32_t head_dim);
+int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
+                    const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                    int32_t max_qo_tokens, int32_t page_size, int32_t num_qo_heads,
+                    int32_t num_kv_heads, int32_t head_dim, int64_t* token_to_page,
+                    int64_t* token_to_cache, int32_t token_map_len, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+int mi_prefill_run(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                   const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                   const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                   int32_t max_qo_tokens, int32_t num_qo_heads, int32_t causal, float sm_scale, void* workspace,
+                   int64_t workspace_bytes, void* out, int64_t out_stride_token,
+                   int64_t out_stride_head, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSTAR_AMD_H */

@@ -1,0 +1,180 @@
+"""ctypes binding of the gfx950 C ABI declared in ``include/mstar_amd.h``.
+
+The library is built in-tree by ``mstar_amd.build`` (``libmstar_amd.so`` next to
+this file).  There is no fallback: if the library is missing or was built for
+a different ABI version, :func:`lib` raises, and every caller fails loudly.
+``torch`` is imported before the library is loaded so that the dynamic linker
+binds our ``libamdhip64.so.7`` dependency to torch's already-loaded HIP
+runtime: torch tensors and these kernels then share one HIP context.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must be loaded before the HIP library, see above)
+
+LIB_PATH = Path(__file__).resolve().parent / "libmstar_amd.so"
+ABI_VERSION = 1
+
+# dtype codes (mstar_amd.h)
+MI_BF16 = 0
+MI_F16 = 1
+MI_F32 = 2
+MI_FP8_E4M3 = 3
+
+MI_OK = 0
+
+TORCH_TO_MI = {
+    torch.bfloat16: MI_BF16,
+    torch.float16: MI_F16,
+    torch.float32: MI_F32,
+    torch.float8_e4m3fn: MI_FP8_E4M3,
+}
+
+
+class MiPagedKV(ctypes.Structure):
+    """Mirror of ``mi_paged_kv`` (mstar_amd.h)."""
+
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("max_pages", ctypes.c_int64),
+        ("page_stride", ctypes.c_int64),
+        ("kv_stride", ctypes.c_int64),
+        ("token_stride", ctypes.c_int64),
+        ("head_stride", ctypes.c_int64),
+        ("k_scale", ctypes.c_void_p),
+        ("v_scale", ctypes.c_void_p),
+    ]
+
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_F32 = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/mstar_amd.h exactly.
+SIGNATURES = {
+    "mi_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "mi_abi_version": (ctypes.c_int, []),
+    "mi_pack": (ctypes.c_int, [_P, _P, _P, _P, _I32, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _P]),
+    "mi_block_table_update": (ctypes.c_int, [_P, _I64, _P, _P, _P, _I32, _P]),
+    "mi_decode_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32]),
+    "mi_decode_plan": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _I64, _P]),
+    "mi_decode_run": (
+        ctypes.c_int,
+        [_P, _I32, _I64, _I64, ctypes.POINTER(MiPagedKV), _P, _P, _P, _P, _I32, _I32, _I32, _F32,
+         _P, _I64, _P, _I64, _I64, _P],
+    ),
+    "mi_decode_attend": (
+        ctypes.c_int,
+        [_P, _I32, _I64, _I64, ctypes.POINTER(MiPagedKV), _P, _P, _P, _P, _I32, _I32, _I32, _F32,
+         _P, _I64, _P, _I64, _I64, _P],
+    ),
+    "mi_decode_merge": (
+        ctypes.c_int,
+        [_P, _I32, _I64, _I64, ctypes.POINTER(MiPagedKV), _P, _P, _P, _P, _I32, _I32, _I32, _F32,
+         _P, _I64, _P, _I64, _I64, _P],
+    ),
+    "mi_kv_append": (
+        ctypes.c_int,
+        [ctypes.POINTER(MiPagedKV), _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _P, _I64, _I32, _P, _P],
+    ),
+    "mi_prefill_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
+    "mi_prefill_plan": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _I32, _P, _I64, _P],
+    ),
+    "mi_prefill_run": (
+        ctypes.c_int,
+        [_P, _I32, _I64, _I64, ctypes.POINTER(MiPagedKV), _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32,
+         _P, _I64, _P, _I64, _I64, _P],
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raise if it is unavailable."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build the gfx950 kernels first "
+                "(python -m mstar_amd.build). There is no CPU fallback."
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = handle.mi_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
+        _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    """Map a nonzero C status to an exception."""
+    if status != MI_OK:
+        text = lib().mi_status_string(status).decode()
+        if status == -1:
+            raise ValueError(f"{what}: {text} (status {status})")
+        raise RuntimeError(f"{what}: {text} (status {status})")
+
+
+def stream_ptr(device: torch.device | None = None) -> int:
+    """Raw hipStream_t of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def paged_kv_desc(kv_cache_layer: torch.Tensor, k_scale: torch.Tensor | None = None,
+                  v_scale: torch.Tensor | None = None) -> MiPagedKV:
+    """Describe one KV layer ``[max_pages, 2, page_size, num_kv_heads, head_dim]``."""
+    if kv_cache_layer.dim() != 5 or kv_cache_layer.shape[1] != 2:
+        raise ValueError(
+            f"kv_cache_layer must be [max_pages, 2, page_size, num_kv_heads, head_dim], got {tuple(kv_cache_layer.shape)}"
+        )
+    if kv_cache_layer.stride(4) != 1:
+        raise ValueError("kv_cache_layer: head_dim must be contiguous")
+    dt = TORCH_TO_MI.get(kv_cache_layer.dtype)
+    if dt is None or dt == MI_F32:
+        raise ValueError(f"unsupported KV cache dtype {kv_cache_layer.dtype} (bf16, fp16 or float8_e4m3fn)")
+    d = MiPagedKV()
+    d.data = kv_cache_layer.data_ptr()
+    d.dtype = dt
+    d.page_size = kv_cache_layer.shape[2]
+    d.num_kv_heads = kv_cache_layer.shape[3]
+    d.head_dim = kv_cache_layer.shape[4]
+    d.max_pages = kv_cache_layer.shape[0]
+    d.page_stride = kv_cache_layer.stride(0)
+    d.kv_stride = kv_cache_layer.stride(1)
+    d.token_stride = kv_cache_layer.stride(2)
+    d.head_stride = kv_cache_layer.stride(3)
+    if dt == MI_FP8_E4M3:
+        if k_scale is None or v_scale is None:
+            raise ValueError("an fp8 KV cache needs per-head k_scale and v_scale tensors")
+        for name, s in (("k_scale", k_scale), ("v_scale", v_scale)):
+            if s.dtype != torch.float32 or s.numel() != d.num_kv_heads or not s.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous float32 tensor of num_kv_heads elements")
+            if s.device != kv_cache_layer.device:
+                raise ValueError(f"{name} must live on the KV cache's device")
+        d.k_scale = k_scale.data_ptr()
+        d.v_scale = v_scale.data_ptr()
+    else:
+        d.k_scale = None
+        d.v_scale = None
+    return d

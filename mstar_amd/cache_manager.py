@@ -1,0 +1,306 @@
+"""BatchedCacheManager with GPU batch packing.
+
+Keeps the methods M*'s model code calls on ``mstar.engine.cache_manager.
+BatchedCacheManager`` (``cache_manager.py:56-881``): ``plan_attention``,
+``run_attention``, ``set_layer_idx``, ``set_active_label(s)``,
+``get_qo_indptr_buf``, ``advance_seq_len(s)``, ``set_custom_pos_advance``,
+``flush_to_store``, plus the pre-planned-label fast path used by the CUDA-graph
+runner (``_pre_planned_labels``, ``cache_manager.py:202-217``).
+
+What changes is how a step is packed (``_plan_attention_impl``,
+``cache_manager.py:229-424``).  The reference walks every request in Python,
+re-flattens every page list into CPU tensors and lets the wrapper copy them to
+the device.  Here the host only allocates pages (same FIFO allocator, same
+batch order, same ``AllocationFailedError``), sends the pages allocated since
+the last step to the device block table, and one GPU kernel (``mi_pack``)
+builds ``qo_indptr``, ``kv_indptr``, ``kv_indices``, ``last_page_len`` and the
+decode write locations.  The wrapper's ``plan()`` then builds its split-KV or
+prefill partition on the GPU from those device tensors.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from .kv_store import KVCacheConfig, KVRequestState, PagedAllocationManager
+from .paged_attention import PagedDecodeWrapper, PagedPrefillWrapper
+
+
+@dataclass
+class _PlanState:
+    """Per-label plan state (``cache_manager.py:9-37``)."""
+
+    wrapper: PagedPrefillWrapper | PagedDecodeWrapper | None = None
+    pos_ids: torch.Tensor | None = None
+    seq_lens: list[int] | None = None
+    write_store: bool = True
+    custom_pos_advance: list[int] | None = None
+
+
+class WorkspaceBufferManager:
+    """One workspace buffer per label (``cache_manager.py:40-53``)."""
+
+    def __init__(self, size: int, device):
+        self.size = size
+        self.device = device
+        self.buffers: dict[str, torch.Tensor] = {}
+
+    def get(self, label: str = "main") -> torch.Tensor:
+        if label not in self.buffers:
+            self.buffers[label] = torch.empty(self.size, dtype=torch.uint8, device=self.device)
+        return self.buffers[label]
+
+
+class _PackBuffers:
+    """Device outputs of mi_pack, reused across steps while they are large enough."""
+
+    def __init__(self, device):
+        self.device = device
+        self.meta: torch.Tensor | None = None
+        self.indices: torch.Tensor | None = None
+        self.locations: torch.Tensor | None = None
+        self.staging: torch.Tensor | None = None
+        self.event: torch.cuda.Event | None = None
+
+    def upload(self, arr: np.ndarray) -> torch.Tensor:
+        n = arr.size
+        if self.staging is None or self.staging.numel() < n:
+            self.staging = torch.empty(max(n, 4096), dtype=torch.int32, pin_memory=True)
+            self.event = None
+        if self.event is not None:
+            self.event.synchronize()
+        self.staging[:n].numpy()[:] = arr
+        dev = torch.empty(n, dtype=torch.int32, device=self.device)
+        dev.copy_(self.staging[:n], non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record()
+        return dev
+
+
+class BatchedCacheManager:
+    """Batched paged attention for the requests of one step (``cache_manager.py:56``)."""
+
+    def __init__(
+        self,
+        request_ids: list[str],
+        active_labels_per_request: dict[str, str],
+        kv_cache: torch.Tensor,
+        alloc_manager: PagedAllocationManager,
+        buffer_manager: WorkspaceBufferManager,
+        kv_cache_config: KVCacheConfig,
+        device,
+        cuda_graph_plan_states: dict[str, _PlanState] | None = None,
+        auto_write_store: bool = False,
+        enable_nvtx: bool = False,
+        kv_scales: torch.Tensor | None = None,
+    ):
+        """``kv_scales`` (extension): fp32 ``[num_layers, 2, num_kv_heads]`` per-head
+        dequantisation scales of an fp8-e4m3 ``kv_cache``."""
+        self.request_ids = request_ids
+        self.active_labels = active_labels_per_request
+        self.kv_cache = kv_cache
+        self.alloc_manager = alloc_manager
+        self.buffer_manager = buffer_manager
+        self.kv_cache_config = kv_cache_config
+        self.device = torch.device(device)
+        self.layer_idx = 0
+        self.enable_nvtx = enable_nvtx
+        self.auto_write_store = auto_write_store
+        self.kv_scales = kv_scales
+        self._cuda_graph_mode = cuda_graph_plan_states is not None
+        self._plan_states: dict[str, _PlanState] = cuda_graph_plan_states if cuda_graph_plan_states is not None else {}
+        self._pre_planned_labels: set[str] = set()
+        self._plan_done_event = None
+        self._pack = _PackBuffers(self.device)
+        if alloc_manager.block_table is None:
+            raise ValueError("the allocation manager needs a device (block table) for GPU packing")
+
+    # ------------------------------------------------------------ labels
+    def _get_state(self, request_id: str, label: str | None = None) -> KVRequestState:
+        label = label or self.active_labels.get(request_id, "main")
+        return self.alloc_manager.get_state(request_id, label)
+
+    def set_active_labels(self, labels: dict[str, str]) -> None:
+        self.active_labels = labels
+
+    def set_active_label(self, label: str) -> None:
+        self.active_labels = {rid: label for rid in self.request_ids}
+
+    def set_layer_idx(self, layer_idx: int) -> None:
+        self.layer_idx = layer_idx
+
+    def get_qo_indptr_buf(self, label: str = "main") -> torch.Tensor | None:
+        ps = self._plan_states.get(label)
+        if ps is None or ps.wrapper is None:
+            return None
+        return getattr(ps.wrapper, "_qo_indptr_buf", None)
+
+    def _single_active_label(self) -> str:
+        labels = list(self.active_labels.values())
+        assert len(set(labels)) == 1, f"All active labels must be the same, got {labels}"
+        return labels[0]
+
+    # ------------------------------------------------------------ planning
+    def plan_attention(self, seq_lens: list[int] | None = None, dtype: torch.dtype | None = None,
+                       is_causal: bool = True, write_store: bool = True, label: str | None = None) -> None:
+        """Allocate pages, pack the step on the GPU and plan the wrapper (``cache_manager.py:167-227``)."""
+        effective = label if label is not None else self._single_active_label()
+        if effective in self._pre_planned_labels:
+            self._pre_planned_labels.discard(effective)
+            ps = self._plan_states.get(effective)
+            if ps is not None:
+                ps.seq_lens = seq_lens
+                ps.write_store = write_store
+            return
+        self._plan_attention_impl(seq_lens, dtype, is_causal, write_store, effective)
+
+    def _plan_attention_impl(self, seq_lens, dtype, is_causal, write_store, label) -> None:
+        assert self.kv_cache is not None
+        if dtype is None:
+            dtype = torch.bfloat16 if self.kv_cache.dtype == torch.float8_e4m3fn else self.kv_cache.dtype
+        cfg = self.kv_cache_config
+        ps_ = cfg.page_size
+        b = len(self.request_ids)
+        if len(seq_lens) != b:
+            raise ValueError(f"{len(seq_lens)} seq_lens for {b} requests")
+        # host: FIFO allocation in batch order (cache_manager.py:278-285); raises
+        # AllocationFailedError before any kernel is launched.
+        states = []
+        meta = np.empty((4, b), dtype=np.int32)
+        for i, rid in enumerate(self.request_ids):
+            st = self._get_state(rid, label)
+            sl = int(seq_lens[i])
+            self.alloc_manager.alloc(rid, label=label, seq_len=st.seq_len + sl)
+            states.append(st)
+            meta[1, i] = st.seq_len
+            meta[2, i] = sl
+            meta[3, i] = len(st.page_indices)
+        bt = self.alloc_manager.block_table
+        bt.sync(states)
+        meta[0] = [st.slot for st in states]
+        total_pages = int(meta[3].sum())
+        is_decode = all(int(s) == 1 for s in seq_lens)
+
+        ps = self._plan_states.get(label)
+        if ps is not None and ps.wrapper is not None:
+            wrapper = ps.wrapper
+        else:
+            cls = PagedDecodeWrapper if is_decode else PagedPrefillWrapper
+            wrapper = cls(
+                workspace_buffer=self.buffer_manager.get(label),
+                num_qo_heads=cfg.num_qo_heads,
+                num_kv_heads=cfg.num_kv_heads,
+                head_dim=cfg.head_dim,
+                page_size=ps_,
+                device=self.device,
+                enable_nvtx=self.enable_nvtx,
+            )
+            ps = _PlanState(wrapper=wrapper)
+            self._plan_states[label] = ps
+
+        # device: one upload of [slot | seq_len | new_len | num_pages], one pack kernel
+        dmeta = self._pack.upload(meta.reshape(-1))
+        graph_static = isinstance(wrapper, PagedDecodeWrapper) and wrapper.use_cuda_graph
+        graph_static_pf = isinstance(wrapper, PagedPrefillWrapper) and wrapper.use_cuda_graph
+        if graph_static or graph_static_pf:
+            qo = wrapper._qo_indptr_buf if graph_static_pf else torch.empty(b + 1, dtype=torch.int32, device=self.device)
+            kv_indptr = wrapper._paged_kv_indptr_buf
+            kv_indices = wrapper._paged_kv_indices_buf
+            last = wrapper._paged_kv_last_page_len_buf
+            if total_pages > kv_indices.shape[0]:
+                raise ValueError(f"{total_pages} pages > wrapper max_num_pages {kv_indices.shape[0]}")
+        else:
+            qo = torch.empty(b + 1, dtype=torch.int32, device=self.device)
+            kv_indptr = torch.empty(b + 1, dtype=torch.int32, device=self.device)
+            kv_indices = torch.empty(max(total_pages, 1), dtype=torch.int32, device=self.device)
+            last = torch.empty(b, dtype=torch.int32, device=self.device)
+        loc = torch.empty(b, 2, dtype=torch.long, device=self.device) if is_decode else None
+        grid = max(1, min(64, (total_pages + 8191) // 8192))
+        base = dmeta.data_ptr()
+        _lib.check(
+            _lib.lib().mi_pack(
+                base, base + 4 * b, base + 8 * b, base + 12 * b, b, bt.table.data_ptr(), bt.stride, ps_,
+                qo.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(), last.data_ptr(),
+                loc.data_ptr() if loc is not None else None, grid, _lib.stream_ptr(self.device),
+            ),
+            "mi_pack",
+        )
+        self._last_pack = (qo, kv_indptr, kv_indices[:total_pages], last, loc)
+        if isinstance(wrapper, PagedDecodeWrapper):
+            wrapper.plan(kv_indptr, kv_indices[:total_pages], last, kv_cache_locations=loc, dtype=dtype)
+        else:
+            wrapper.plan_device(qo, kv_indptr, kv_indices[:total_pages], last, total_tokens=int(meta[2].sum()),
+                                causal=is_causal, dtype=dtype)
+        ps.seq_lens = list(seq_lens)
+        ps.write_store = write_store
+
+    # ------------------------------------------------------------ running
+    def _layer_scales(self, layer_idx: int):
+        if self.kv_scales is None:
+            return None, None
+        return self.kv_scales[layer_idx, 0], self.kv_scales[layer_idx, 1]
+
+    def run_attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      layer_idx: int | None = None) -> torch.Tensor:
+        """Append this step's K/V, then attend (``cache_manager.py:653-701``)."""
+        if layer_idx is None:
+            layer_idx = self.layer_idx
+        orig_dtype = q.dtype
+        label = self._single_active_label()
+        ps = self._plan_states[label]
+        assert self.kv_cache is not None and ps.wrapper is not None
+        layer = self.kv_cache[layer_idx]
+        ks, vs = self._layer_scales(layer_idx)
+        ps.wrapper.set_kv_cache(layer, k, v, ks, vs)
+        if self.auto_write_store and ps.write_store:
+            for rid in self.request_ids:
+                self.alloc_manager.flush_to_store(rid, label=label, layers=layer_idx)
+        return ps.wrapper.run(q, layer, ks, vs).to(orig_dtype)
+
+    # ------------------------------------------------------------ advance
+    def advance_seq_len(self, n: int | None = None, pos_id_n: int | None = None) -> None:
+        if n is None:
+            return self.advance_seq_lens(pos_id_n)
+        for rid in self.request_ids:
+            st = self._get_state(rid)
+            st.seq_len += n
+            st.position_id_start += pos_id_n if pos_id_n is not None else n
+
+    def set_custom_pos_advance(self, pos_advance: list[int] | None, label: str | None = None) -> None:
+        if label is None:
+            labels = list(self.active_labels.values())
+            if not labels:
+                return
+            assert len(set(labels)) == 1, f"All active labels must be the same to omit ``label``, got {labels}"
+            label = labels[0]
+        ps = self._plan_states.get(label)
+        if ps is not None:
+            ps.custom_pos_advance = list(pos_advance) if pos_advance is not None else None
+
+    def advance_seq_lens(self, pos_id_ns: list[int] | int | None = None) -> None:
+        """``seq_len += seq_lens[i]`` per request (``cache_manager.py:811-838``)."""
+        for i, rid in enumerate(self.request_ids):
+            ps = self._plan_states[self.active_labels[rid]]
+            n = ps.seq_lens[i]
+            st = self._get_state(rid)
+            st.seq_len += n
+            if pos_id_ns is None:
+                st.position_id_start += ps.custom_pos_advance[i] if ps.custom_pos_advance is not None else n
+            elif isinstance(pos_id_ns, int):
+                st.position_id_start += pos_id_ns
+            else:
+                st.position_id_start += pos_id_ns[i]
+        for ps in self._plan_states.values():
+            ps.custom_pos_advance = None
+
+    def flush_to_store(self) -> None:
+        for rid in self.request_ids:
+            for label in self.alloc_manager.request_states[rid]:
+                ps = self._plan_states.get(label)
+                if ps is None or not ps.write_store:
+                    continue
+                self.alloc_manager.flush_to_store(rid, label)

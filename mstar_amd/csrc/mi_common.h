@@ -1,0 +1,151 @@
+// Shared device/host helpers for the MI355X (gfx950) paged-attention kernels.
+//
+// Everything here is written for CDNA4: 64-lane wavefronts, MFMA matrix
+// cores (v_mfma_f32_16x16x32_{bf16,f16}, v_mfma_f32_16x16x16{bf16_1k,f16}),
+// and 128-bit global loads.  No other target is supported.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mstar_amd.h"
+
+#define MI_DEVICE __device__ __forceinline__
+
+namespace mi {
+
+constexpr int kWave = 64;
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+
+// ---------------------------------------------------------------- bit casts
+template <typename To, typename From>
+MI_DEVICE To bitcast(const From& v) {
+  static_assert(sizeof(To) == sizeof(From), "bitcast size mismatch");
+  return __builtin_bit_cast(To, v);
+}
+
+// ------------------------------------------------------- scalar conversions
+// float -> bfloat16 bits, round-to-nearest-even; NaN -> 0x7FC0 (canonical
+// quiet NaN with the input's sign dropped), the same result torch's
+// Tensor.to(torch.bfloat16) produces on the CPU.
+MI_DEVICE uint16_t f32_to_bf16_rne(float x) {
+  uint32_t u = bitcast<uint32_t>(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+MI_DEVICE float bf16_to_f32(uint16_t h) { return bitcast<float>((uint32_t)h << 16); }
+
+// float -> fp16 bits, round-to-nearest-even (hardware v_cvt_f16_f32 uses the
+// default RNE mode; overflow -> inf, NaN -> NaN).
+MI_DEVICE uint16_t f32_to_f16_rne(float x) { return bitcast<uint16_t>((_Float16)x); }
+MI_DEVICE float f16_to_f32(uint16_t h) { return (float)bitcast<_Float16>(h); }
+
+// float -> OCP fp8 e4m3fn (bias 7, no infinities, 0x7F/0xFF = NaN, max 448).
+// Round-to-nearest-even.  Magnitudes that round past 448 (>= 464) and NaN
+// map to NaN, matching torch's non-saturating float8_e4m3fn cast; callers
+// clamp to +-448 first.
+MI_DEVICE uint8_t f32_to_e4m3fn(float x) {
+  const uint32_t u = bitcast<uint32_t>(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a >= 0x43e80000u) return (uint8_t)(sign | 0x7fu);  // >= 464.0 or NaN/inf
+  if (a < 0x3c800000u) {                                  // < 2^-6: subnormal grid 2^-9
+    const float q = __builtin_rintf(bitcast<float>(a) * 512.0f);  // exact scale, RNE
+    return (uint8_t)(sign | (uint32_t)q);                 // q == 8 encodes 2^-6
+  }
+  uint32_t e = (a >> 23) - 120u;  // rebias 127 -> 7, in [1, 15]
+  uint32_t m = (a >> 20) & 7u;
+  const uint32_t rem = a & 0xfffffu;
+  if (rem > 0x80000u || (rem == 0x80000u && (m & 1u))) {
+    if (++m == 8u) { m = 0u; ++e; }
+  }
+  return (uint8_t)(sign | (e << 3) | m);
+}
+
+// ------------------------------------------------------------ type traits
+// 16-bit floating storage types handled by the MFMA paths.
+struct BF16 {
+  static constexpr int kDtype = MI_BF16;
+  MI_DEVICE static float to_f32(uint16_t h) { return bf16_to_f32(h); }
+  MI_DEVICE static uint16_t from_f32(float x) { return f32_to_bf16_rne(x); }
+  // Two floats -> packed pair, RNE (hardware v_cvt_pk_bf16_f32 on gfx950).
+  MI_DEVICE static uint32_t pack2(float a, float b) {
+    return (uint32_t)bitcast<uint16_t>((__bf16)a) | ((uint32_t)bitcast<uint16_t>((__bf16)b) << 16);
+  }
+  // S^T tile product: A = 16x32 (8 elems/lane), B = 32x16, C = 16x16 fp32.
+  MI_DEVICE static f32x4 mma_16x16x32(const uint4& a, const uint4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c, 0, 0, 0);
+  }
+  // A = 16x16 (4 elems/lane), B = 16x16, C = 16x16 fp32.
+  MI_DEVICE static f32x4 mma_16x16x16(const uint2& a, const uint2& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bitcast<i16x4>(a), bitcast<i16x4>(b), c, 0, 0, 0);
+  }
+};
+
+struct F16 {
+  static constexpr int kDtype = MI_F16;
+  MI_DEVICE static float to_f32(uint16_t h) { return f16_to_f32(h); }
+  MI_DEVICE static uint16_t from_f32(float x) { return f32_to_f16_rne(x); }
+  MI_DEVICE static uint32_t pack2(float a, float b) {
+    return (uint32_t)bitcast<uint16_t>((_Float16)a) | ((uint32_t)bitcast<uint16_t>((_Float16)b) << 16);
+  }
+  MI_DEVICE static f32x4 mma_16x16x32(const uint4& a, const uint4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<f16x8>(a), bitcast<f16x8>(b), c, 0, 0, 0);
+  }
+  MI_DEVICE static f32x4 mma_16x16x16(const uint2& a, const uint2& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(bitcast<f16x4>(a), bitcast<f16x4>(b), c, 0, 0, 0);
+  }
+};
+
+// fp8 e4m3fn pair (selected 16-bit half of `w`) -> packed 16-bit pair of the
+// MFMA type, exact (gfx950 hardware conversion, scale 1.0).
+template <typename MT>
+MI_DEVICE uint32_t fp8x2_to_mt(uint32_t w, bool hi);
+template <>
+MI_DEVICE uint32_t fp8x2_to_mt<BF16>(uint32_t w, bool hi) {
+  return hi ? bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true))
+            : bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+}
+template <>
+MI_DEVICE uint32_t fp8x2_to_mt<F16>(uint32_t w, bool hi) {
+  return hi ? bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true))
+            : bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+}
+
+// ------------------------------------------------------------ lane helpers
+MI_DEVICE int lane_id() { return __lane_id(); }
+
+// Wave-uniform value in an SGPR.
+MI_DEVICE int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+MI_DEVICE float xor_shuffle(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// v_perm_b32: byte i of the result = byte sel[i] of {hi:lo} where selector
+// values 0-3 address `lo` and 4-7 address `hi`.
+MI_DEVICE uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+// (lo16(a), lo16(b)) and (hi16(a), hi16(b)) packs.
+MI_DEVICE uint32_t pack_lo16(uint32_t a, uint32_t b) { return perm_b32(b, a, 0x05040100u); }
+MI_DEVICE uint32_t pack_hi16(uint32_t a, uint32_t b) { return perm_b32(b, a, 0x07060302u); }
+
+MI_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+MI_DEVICE float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+}  // namespace mi
+
+// ------------------------------------------------------------ host helpers
+#define MI_CHECK_LAUNCH()                                   \
+  do {                                                      \
+    hipError_t _e = hipGetLastError();                      \
+    if (_e != hipSuccess) return MI_ERR_LAUNCH;             \
+  } while (0)
+
+static inline int64_t mi_align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }

@@ -1,0 +1,656 @@
+// Split-KV paged GQA decode for MI355X (gfx950).
+//
+// Replaces FlashInfer's BatchDecodeWithPagedKVCacheWrapper plan/run as used by
+// FlashInferDecodeWrapper (mstar/utils/flashinfer_utils.py:369-465), and the
+// short-query part of the prefill wrapper (requests whose
+// qo_len * group <= 16).
+//
+// Work decomposition
+//   plan  : one 1024-thread workgroup splits every request's page list into
+//           chunks of `chunk_pages` pages (chunk_pages chosen on the GPU from
+//           the batch's total page count so the machine gets ~8K wave units)
+//           and writes the chunk list into the caller's workspace.
+//   decode: one wavefront per (chunk, kv-head).  Its 16 MFMA columns are the
+//           (query token, q-head-in-group) rows that share that kv-head, so
+//           K/V are loaded from HBM once per GQA group.  Per 16-token tile:
+//             S^T[16 tok x 16 rows] = K[16 x D] . Q^T      (v_mfma 16x16x32)
+//             online softmax on S (fp32, exp2 domain)
+//             O^T[D x 16 rows]     += V^T[D x 16 tok] . P^T (v_mfma 16x16x16)
+//           K rows are read as 64-byte row segments, V rows as whole
+//           head_dim rows (D*2 bytes) per 16 lanes: every 128-bit load is
+//           fully used.  V is transposed in registers (v_perm_b32): output
+//           column d is permuted as d = (D/16)*m + tile, which turns the
+//           transpose into a 4x(D/16) shuffle inside each lane.
+//   merge : log-sum-exp merge of the chunk partials of split requests.
+#include <stdlib.h>
+
+#include "mi_common.h"
+#include "mi_internal.h"
+
+namespace mi {
+
+constexpr int kRows = 16;             // MFMA N: query rows per wave
+constexpr int kMinChunkTokens = 256;  // never split a request finer than this
+
+
+// Target number of KV chunks for one plan: ~8K (chunk, kv-head) wave units
+// keeps 256 CUs x 4 SIMDs busy with a short tail.  MSTAR_DECODE_TARGET_UNITS
+// overrides it for tuning sweeps (read once per process).
+static int32_t decode_target_units() {
+  static const int32_t units = [] {
+    const char* e = getenv("MSTAR_DECODE_TARGET_UNITS");
+    int v = e ? atoi(e) : 8192;
+    return v < 64 ? 64 : v;
+  }();
+  return units;
+}
+
+SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t ws_avail) {
+  SplitLayout L;
+  int32_t target = decode_target_units() / (nkv > 0 ? nkv : 1);
+  if (target < 16) target = 16;
+  int64_t max_chunks = (int64_t)target + batch;
+  if (ws_avail >= 0) {  // fewer, longer chunks when the caller's workspace is smaller
+    const int64_t fixed = 256 + mi_align_up(4LL * (batch + 1), 256) + 3 * 256;
+    const int64_t per_chunk = 16 + 4LL * nkv * kRows + 4LL * nkv * kRows * head_dim;
+    const int64_t fit = (ws_avail - fixed) / per_chunk;
+    if (fit < max_chunks) max_chunks = fit;
+  }
+  L.max_chunks = (int32_t)max_chunks;
+  int64_t off = 0;
+  L.hdr = off;
+  off += 256;
+  L.chunk_indptr = off;
+  off = mi_align_up(off + 4LL * (batch + 1), 256);
+  L.work = off;
+  off = mi_align_up(off + 16LL * L.max_chunks, 256);
+  L.lse = off;
+  off = mi_align_up(off + 4LL * L.max_chunks * nkv * kRows, 256);
+  L.opart = off;
+  off = mi_align_up(off + 4LL * L.max_chunks * nkv * kRows * head_dim, 256);
+  L.total = off;
+  return L;
+}
+
+// Header words written by the plan kernel.
+enum { kHdrMagic = 0, kHdrBatch, kHdrChunks, kHdrChunkPages, kHdrMaxChunks };
+constexpr int32_t kPlanMagic = 0x4d494450;
+
+struct PlanParams {
+  const int32_t* qo_indptr;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* last_page_len;
+  int32_t batch, target, min_chunk_pages, max_chunks, group;
+  int32_t* hdr;
+  int32_t* chunk_indptr;
+  int4* work;
+  int64_t* kv_locations;
+};
+
+__global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
+  __shared__ int smem[16];
+  const int total_pages = p.kv_indptr[p.batch] - p.kv_indptr[0];
+  int cp = (total_pages + p.target - 1) / p.target;
+  if (cp < p.min_chunk_pages) cp = p.min_chunk_pages;
+  int carry = 0;
+  for (int base = 0; base < p.batch; base += 1024) {
+    const int b = base + (int)threadIdx.x;
+    int np = 0, n = 0;
+    if (b < p.batch) {
+      np = p.kv_indptr[b + 1] - p.kv_indptr[b];
+      n = np > 0 ? (np + cp - 1) / cp : 0;
+      if (p.qo_indptr) {  // ragged batch: only short-query requests belong to this kernel
+        const int qo_len = p.qo_indptr[b + 1] - p.qo_indptr[b];
+        if (qo_len <= 0 || qo_len * p.group > kRows) n = 0;
+      }
+    }
+    int total;
+    const int first = block_exclusive_scan_1024(n, total, smem) + carry;
+    if (b < p.batch) {
+      p.chunk_indptr[b] = first;
+      for (int c = 0; c < n && first + c < p.max_chunks; ++c) {
+        const int p0 = c * cp;
+        p.work[first + c] = make_int4(b, p0, min(p0 + cp, np), n);
+      }
+      if (p.kv_locations) {
+        int64_t page = -1, pos = -1;
+        if (np > 0) {
+          page = p.kv_indices[p.kv_indptr[b + 1] - 1];
+          pos = p.last_page_len[b] - 1;
+        }
+        p.kv_locations[2 * b] = page;
+        p.kv_locations[2 * b + 1] = pos;
+      }
+    }
+    carry += total;
+  }
+  if (threadIdx.x == 0) {
+    p.chunk_indptr[p.batch] = carry;
+    p.hdr[kHdrMagic] = kPlanMagic;
+    p.hdr[kHdrBatch] = p.batch;
+    p.hdr[kHdrChunks] = min(carry, p.max_chunks);
+    p.hdr[kHdrChunkPages] = cp;
+    p.hdr[kHdrMaxChunks] = p.max_chunks;
+  }
+}
+
+// ---------------------------------------------------------------- decode
+struct DecodeParams {
+  const void* q;
+  int64_t q_stride_tok, q_stride_head;
+  const void* kv;
+  int64_t page_stride, kv_stride, token_stride, head_stride;
+  const float* k_scale;
+  const float* v_scale;
+  const int32_t* qo_indptr;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* last_page_len;
+  const int32_t* hdr;
+  const int4* work;
+  const int32_t* chunk_indptr;
+  float* lse_part;
+  float* o_part;
+  void* out;
+  int64_t out_stride_tok, out_stride_head;
+  int32_t num_kv_heads, group, page_size, causal;
+  float scale_log2;
+};
+
+// Per-lane registers of one 16-token tile.
+template <bool FP8, int D>
+struct TileRegs;
+
+template <int D>
+struct TileRegs<false, D> {  // 16-bit KV: K as MFMA A fragments, V as row slices
+  uint4 k[D / 32];
+  uint32_t v[4][D / 32];  // D/16 elements (16-bit) per row
+};
+
+template <int D>
+struct TileRegs<true, D> {  // fp8 KV: raw bytes, converted right before use
+  uint2 k[D / 32];
+  uint32_t v[4][D / 64 > 0 ? D / 64 : 1];  // D/16 bytes per row
+};
+
+template <int N>
+MI_DEVICE void load_words(uint32_t (&dst)[N], const uint8_t* src) {
+  if constexpr (N == 1) {
+    dst[0] = *(const uint32_t*)src;
+  } else if constexpr (N == 2) {
+    const uint2 t = *(const uint2*)src;
+    dst[0] = t.x;
+    dst[1] = t.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      const uint4 t = *(const uint4*)(src + 4 * i);
+      dst[i] = t.x;
+      dst[i + 1] = t.y;
+      dst[i + 2] = t.z;
+      dst[i + 3] = t.w;
+    }
+  }
+}
+
+template <typename MT, bool FP8, int D>
+__global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
+  constexpr int KS = D / 32;  // MFMA k-steps over head_dim for S
+  constexpr int VW = D / 16;  // V elements per lane per row == output d-tiles
+  constexpr int ESZ = FP8 ? 1 : 2;
+  constexpr float kNegInf = -__builtin_inff();
+
+  const int lane = lane_id();
+  const int wave = uniform((int)threadIdx.x >> 6);
+  const int nkv = p.num_kv_heads;
+  const int unit = (int)blockIdx.x * 4 + wave;
+  const int chunk = uniform(unit / nkv);
+  const int h = unit - chunk * nkv;
+  if (chunk >= p.hdr[kHdrChunks]) return;
+  const int4 wk = p.work[chunk];
+  const int b = uniform(wk.x), pg0 = uniform(wk.y), pg1 = uniform(wk.z), nchunks_b = uniform(wk.w);
+
+  const int ps = p.page_size;
+  const int page_base = p.kv_indptr[b];
+  const int np = p.kv_indptr[b + 1] - page_base;
+  const int kv_len = (np - 1) * ps + p.last_page_len[b];
+  int qo_start = b, qo_len = 1;
+  if (p.qo_indptr) {
+    qo_start = p.qo_indptr[b];
+    qo_len = p.qo_indptr[b + 1] - qo_start;
+  }
+  const int G = p.group;
+  const int rows = min(qo_len * G, kRows);
+  const int tok_begin = pg0 * ps;
+  const int tok_end = min(pg1 * ps, kv_len);
+  const int ntiles = tok_end > tok_begin ? (tok_end - tok_begin + 15) >> 4 : 0;
+
+  const int col = lane & 15;  // query row handled in MFMA column `col`
+  const int grp = lane >> 4;  // 0..3
+  const int qtok = col / G;
+  const int g = col - qtok * G;
+  const bool row_valid = col < rows;
+  // Keys this row may attend: [0, lim]  (causal: aligned to the end of the KV).
+  int lim = p.causal ? (kv_len - qo_len + qtok) : (kv_len - 1);
+  lim = min(lim, kv_len - 1);
+  // Keys >= mask_from need a per-row check (uniform bound).
+  const int mask_from = p.causal ? (kv_len - qo_len + 1) : kv_len;
+
+  // ---- Q as the B operand of S^T = K Q^T: lane holds Q[row col][8*grp + 32*s ...]
+  uint4 qf[KS];
+  {
+    const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(qo_start + qtok) * p.q_stride_tok +
+                           (int64_t)(h * G + g) * p.q_stride_head;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qf[s] = row_valid ? *(const uint4*)(qrow + 32 * s + 8 * grp) : make_uint4(0, 0, 0, 0);
+  }
+  float kscale = 1.0f, vscale = 1.0f;
+  if constexpr (FP8) {
+    kscale = p.k_scale[h];
+    vscale = p.v_scale[h];
+  }
+  const float sl2 = p.scale_log2 * kscale;
+
+  const uint8_t* kv = (const uint8_t*)p.kv;
+  const int64_t head_off = (int64_t)h * p.head_stride * ESZ;
+  // per-lane byte offsets inside a tile (relative to the tile's first K row)
+  const uint32_t koff = (uint32_t)(col * p.token_stride + 8 * grp) * ESZ;
+  const uint32_t voff0 = (uint32_t)((4 * grp) * p.token_stride + VW * col) * ESZ;
+  const uint32_t vrow = (uint32_t)(p.token_stride * ESZ);
+  const int64_t kvhalf = p.kv_stride * ESZ;
+
+  auto tile_base = [&](int page, int r0) -> const uint8_t* {
+    return kv + (int64_t)page * p.page_stride * ESZ + (int64_t)r0 * p.token_stride * ESZ + head_off;
+  };
+  auto load_tile = [&](TileRegs<FP8, D>& t, const uint8_t* base) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if constexpr (FP8)
+        t.k[s] = *(const uint2*)(base + koff + 32 * s);
+      else
+        t.k[s] = *(const uint4*)(base + koff + 64 * s);
+    }
+    const uint8_t* vb = base + kvhalf + voff0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) load_words(t.v[r], vb + r * vrow);
+  };
+  // Page ids of the chunk, 64 at a time in a VGPR (lane i: page pg0+win+i);
+  // v_readlane hands the tile's page to the scalar unit without a memory
+  // round trip inside the pipelined loop.
+  int win = 0;
+  auto load_window = [&](int w0) -> int {
+    const int idx = pg0 + w0 + lane;
+    return idx < pg1 ? p.kv_indices[page_base + idx] : 0;
+  };
+  int pwin = load_window(0);
+  auto page_of_tile = [&](int t) -> int {
+    const int local = (16 * t) / ps;  // tok_begin is page aligned
+    if (local - win >= 64) {
+      win += 64;
+      pwin = load_window(win);
+    }
+    return __builtin_amdgcn_readlane(pwin, local - win);
+  };
+  auto row0_of_tile = [&](int t) -> int { return (16 * t) % ps; };
+
+  f32x4 acc[VW];
+#pragma unroll
+  for (int j = 0; j < VW; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegInf, l_run = 0.f;
+
+  auto compute_tile = [&](TileRegs<FP8, D>& t, int ti) {
+    const int tb = tok_begin + 16 * ti;
+    // ---- S^T = K . Q^T
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      uint4 a;
+      if constexpr (FP8) {
+        a.x = fp8x2_to_mt<MT>(t.k[st].x, false);
+        a.y = fp8x2_to_mt<MT>(t.k[st].x, true);
+        a.z = fp8x2_to_mt<MT>(t.k[st].y, false);
+        a.w = fp8x2_to_mt<MT>(t.k[st].y, true);
+      } else {
+        a = t.k[st];
+      }
+      s = MT::mma_16x16x32(a, qf[st], s);
+    }
+    float sv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sv[r] = s[r] * sl2;
+    const bool need_mask = tb + 16 > mask_from;
+    if (need_mask) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = tb + 4 * grp + r;
+        if (key > lim) sv[r] = kNegInf;
+        if (key >= kv_len) {  // slots past the end hold stale data: keep NaN/Inf out of P.V
+#pragma unroll
+          for (int i = 0; i < (int)(sizeof(t.v[r]) / 4); ++i) t.v[r][i] = 0u;
+        }
+      }
+    }
+    // ---- online softmax (row = col; the 4 lane groups share a row)
+    float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mt = fmaxf(mt, xor_shuffle(mt, 16));
+    mt = fmaxf(mt, xor_shuffle(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(sv[r] - m_use);
+    l_run = l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+    if (__builtin_amdgcn_ballot_w64(m_new > m_run)) {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) acc[j] *= alpha;
+    }
+    m_run = m_new;
+    const uint2 pb = make_uint2(MT::pack2(pr[0], pr[1]), MT::pack2(pr[2], pr[3]));
+    // ---- O^T += V^T . P^T, V transposed in registers
+    uint32_t vv[4][VW / 2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if constexpr (FP8) {
+#pragma unroll
+        for (int i = 0; i < VW / 4; ++i) {
+          vv[r][2 * i] = fp8x2_to_mt<MT>(t.v[r][i], false);
+          vv[r][2 * i + 1] = fp8x2_to_mt<MT>(t.v[r][i], true);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < VW / 2; ++i) vv[r][i] = t.v[r][i];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < VW; ++j) {
+      uint2 a;
+      if (j & 1) {
+        a.x = pack_hi16(vv[0][j >> 1], vv[1][j >> 1]);
+        a.y = pack_hi16(vv[2][j >> 1], vv[3][j >> 1]);
+      } else {
+        a.x = pack_lo16(vv[0][j >> 1], vv[1][j >> 1]);
+        a.y = pack_lo16(vv[2][j >> 1], vv[3][j >> 1]);
+      }
+      acc[j] = MT::mma_16x16x16(a, pb, acc[j]);
+    }
+  };
+
+  // ---- software-pipelined tile loop: loads of tile t+1 overlap compute of t
+  if (ntiles > 0) {
+    TileRegs<FP8, D> A, B;
+    int pg_next = page_of_tile(0);
+    load_tile(A, tile_base(pg_next, row0_of_tile(0)));
+    if (ntiles > 1) pg_next = page_of_tile(1);
+    int t = 0;
+    for (; t + 1 < ntiles; t += 2) {
+      load_tile(B, tile_base(pg_next, row0_of_tile(t + 1)));
+      if (t + 2 < ntiles) pg_next = page_of_tile(t + 2);
+      compute_tile(A, t);
+      if (t + 2 < ntiles) {
+        load_tile(A, tile_base(pg_next, row0_of_tile(t + 2)));
+        if (t + 3 < ntiles) pg_next = page_of_tile(t + 3);
+      }
+      compute_tile(B, t + 1);
+    }
+    if (t < ntiles) compute_tile(A, t);
+  }
+
+  // ---- epilogue
+  float l_tot = l_run + xor_shuffle(l_run, 16);
+  l_tot += xor_shuffle(l_tot, 32);
+  const float inv = l_tot > 0.f ? vscale / l_tot : 0.f;
+  if (!row_valid) return;
+  if (nchunks_b == 1) {
+    uint16_t* orow = (uint16_t*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
+                     (int64_t)(h * G + g) * p.out_stride_head;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      uint32_t w[VW / 2];
+#pragma unroll
+      for (int i = 0; i < VW / 2; ++i) w[i] = MT::pack2(acc[2 * i][r] * inv, acc[2 * i + 1][r] * inv);
+      uint16_t* dst = orow + VW * (4 * grp + r);
+      if constexpr (VW == 4) {
+        *(uint2*)dst = make_uint2(w[0], w[1]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+      }
+    }
+  } else {
+    const int64_t pi = ((int64_t)chunk * nkv + h) * kRows + col;
+    float* orow = p.o_part + pi * D;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float* dst = orow + VW * (4 * grp + r);
+#pragma unroll
+      for (int j = 0; j < VW; j += 4)
+        *(float4*)(dst + j) = make_float4(acc[j][r] * inv, acc[j + 1][r] * inv, acc[j + 2][r] * inv,
+                                          acc[j + 3][r] * inv);
+    }
+    if (grp == 0) p.lse_part[pi] = l_tot > 0.f ? m_run + fast_log2(l_tot) : kNegInf;
+  }
+}
+
+// ----------------------------------------------------------------- merge
+// One workgroup per (request, kv-head): 16 rows x D, 16 threads per row.
+template <typename MT, int D>
+__global__ __launch_bounds__(256) void merge_kernel(DecodeParams p) {
+  constexpr int VW = D / 16;
+  constexpr float kNegInf = -__builtin_inff();
+  const int nkv = p.num_kv_heads;
+  const int b = (int)blockIdx.x / nkv;
+  const int h = (int)blockIdx.x - b * nkv;
+  const int c0 = p.chunk_indptr[b];
+  const int nb = p.chunk_indptr[b + 1] - c0;
+  if (nb == 1) return;  // written directly by the decode kernel
+  int qo_start = b, qo_len = 1;
+  if (p.qo_indptr) {
+    qo_start = p.qo_indptr[b];
+    qo_len = p.qo_indptr[b + 1] - qo_start;
+  }
+  const int G = p.group;
+  if (qo_len * G > kRows) return;  // long-query request: written by the prefill kernel
+  const int rows = qo_len * G;
+  const int n = (int)threadIdx.x >> 4;
+  const int seg = (int)threadIdx.x & 15;
+  if (n >= rows) return;
+  const int qtok = n / G, g = n - qtok * G;
+  float acc[VW];
+#pragma unroll
+  for (int i = 0; i < VW; ++i) acc[i] = 0.f;
+  float M = kNegInf;
+  for (int c = 0; c < nb; ++c) M = fmaxf(M, p.lse_part[((int64_t)(c0 + c) * nkv + h) * kRows + n]);
+  float wsum = 0.f;
+  if (M != kNegInf) {
+    for (int c = 0; c < nb; ++c) {
+      const int64_t pi = ((int64_t)(c0 + c) * nkv + h) * kRows + n;
+      const float wgt = fast_exp2(p.lse_part[pi] - M);
+      wsum += wgt;
+      const float* src = p.o_part + pi * D + VW * seg;
+#pragma unroll
+      for (int i = 0; i < VW; i += 4) {
+        const float4 o = *(const float4*)(src + i);
+        acc[i] += wgt * o.x;
+        acc[i + 1] += wgt * o.y;
+        acc[i + 2] += wgt * o.z;
+        acc[i + 3] += wgt * o.w;
+      }
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  uint16_t* dst = (uint16_t*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
+                  (int64_t)(h * G + g) * p.out_stride_head + VW * seg;
+  uint32_t w[VW / 2];
+#pragma unroll
+  for (int i = 0; i < VW / 2; ++i) w[i] = MT::pack2(acc[2 * i] * inv, acc[2 * i + 1] * inv);
+  if constexpr (VW == 4) {
+    *(uint2*)dst = make_uint2(w[0], w[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+  }
+}
+
+// ------------------------------------------------------------ host side
+static bool supported_head_dim(int d) { return d == 64 || d == 128 || d == 256; }
+
+int decode_plan_impl(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                     const int32_t* last_page_len, int32_t batch, int32_t page_size,
+                     int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int64_t* kv_locations, void* workspace, int64_t workspace_bytes,
+                     int64_t ws_offset, hipStream_t stream) {
+  if (batch < 0 || !kv_indptr || !last_page_len || !workspace) return MI_ERR_INVALID;
+  if (batch > 0 && !kv_indices) return MI_ERR_INVALID;
+  if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads) return MI_ERR_INVALID;
+  if (num_qo_heads / num_kv_heads > kRows) return MI_ERR_UNSUPPORTED;
+  if (page_size <= 0) return MI_ERR_INVALID;
+  if (page_size % 16) return MI_ERR_UNSUPPORTED;
+  if (!supported_head_dim(head_dim)) return MI_ERR_UNSUPPORTED;
+  const SplitLayout L = split_layout(batch, num_kv_heads, head_dim, workspace_bytes - ws_offset);
+  if (L.max_chunks <= batch || workspace_bytes < ws_offset + L.total) return MI_ERR_WORKSPACE;
+  uint8_t* ws = (uint8_t*)workspace + ws_offset;
+  PlanParams pp;
+  pp.qo_indptr = qo_indptr;
+  pp.kv_indptr = kv_indptr;
+  pp.kv_indices = kv_indices;
+  pp.last_page_len = last_page_len;
+  pp.batch = batch;
+  pp.target = L.max_chunks - batch;
+  pp.min_chunk_pages = (kMinChunkTokens + page_size - 1) / page_size;
+  pp.max_chunks = L.max_chunks;
+  pp.group = num_qo_heads / num_kv_heads;
+  pp.hdr = (int32_t*)(ws + L.hdr);
+  pp.chunk_indptr = (int32_t*)(ws + L.chunk_indptr);
+  pp.work = (int4*)(ws + L.work);
+  pp.kv_locations = kv_locations;
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, pp);
+  MI_CHECK_LAUNCH();
+  return MI_OK;
+}
+
+template <typename MT, bool FP8, int D>
+static void launch_decode(const DecodeParams& dp, int grid, int batch, int phases, hipStream_t stream) {
+  if (phases & kPhaseAttend)
+    hipLaunchKernelGGL((decode_kernel<MT, FP8, D>), dim3(grid), dim3(256), 0, stream, dp);
+  if ((phases & kPhaseMerge) && batch > 0)
+    hipLaunchKernelGGL((merge_kernel<MT, D>), dim3(batch * dp.num_kv_heads), dim3(256), 0, stream, dp);
+}
+
+template <typename MT, bool FP8>
+static int dispatch_d(const DecodeParams& dp, int head_dim, int grid, int batch, int phases, hipStream_t stream) {
+  switch (head_dim) {
+    case 64: launch_decode<MT, FP8, 64>(dp, grid, batch, phases, stream); break;
+    case 128: launch_decode<MT, FP8, 128>(dp, grid, batch, phases, stream); break;
+    case 256: launch_decode<MT, FP8, 256>(dp, grid, batch, phases, stream); break;
+    default: return MI_ERR_UNSUPPORTED;
+  }
+  return MI_OK;
+}
+
+int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                    const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                    const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                    int32_t num_qo_heads, int32_t causal, float sm_scale, void* workspace,
+                    int64_t workspace_bytes, int64_t ws_offset, void* out,
+                    int64_t out_stride_token, int64_t out_stride_head, int phases, hipStream_t stream) {
+  if (!kv || batch < 0 || !workspace) return MI_ERR_INVALID;
+  if (batch == 0) return MI_OK;
+  if (!q || !out || !kv->data || !kv_indptr || !kv_indices || !last_page_len) return MI_ERR_INVALID;
+  const int nkv = kv->num_kv_heads, D = kv->head_dim;
+  if (nkv <= 0 || num_qo_heads <= 0 || num_qo_heads % nkv) return MI_ERR_INVALID;
+  if (num_qo_heads / nkv > kRows) return MI_ERR_UNSUPPORTED;
+  if (kv->page_size <= 0) return MI_ERR_INVALID;
+  if (kv->page_size % 16 || !supported_head_dim(D)) return MI_ERR_UNSUPPORTED;
+  const bool fp8 = kv->dtype == MI_FP8_E4M3;
+  if (q_dtype != MI_BF16 && q_dtype != MI_F16) return MI_ERR_UNSUPPORTED;
+  if (!fp8 && kv->dtype != q_dtype) return MI_ERR_UNSUPPORTED;
+  if (fp8 && (!kv->k_scale || !kv->v_scale)) return MI_ERR_INVALID;
+  const SplitLayout L = split_layout(batch, nkv, D, workspace_bytes - ws_offset);
+  if (L.max_chunks <= batch || workspace_bytes < ws_offset + L.total) return MI_ERR_WORKSPACE;
+  uint8_t* ws = (uint8_t*)workspace + ws_offset;
+
+  DecodeParams dp;
+  dp.q = q;
+  dp.q_stride_tok = q_stride_token;
+  dp.q_stride_head = q_stride_head;
+  dp.kv = kv->data;
+  dp.page_stride = kv->page_stride;
+  dp.kv_stride = kv->kv_stride;
+  dp.token_stride = kv->token_stride;
+  dp.head_stride = kv->head_stride;
+  dp.k_scale = kv->k_scale;
+  dp.v_scale = kv->v_scale;
+  dp.qo_indptr = qo_indptr;
+  dp.kv_indptr = kv_indptr;
+  dp.kv_indices = kv_indices;
+  dp.last_page_len = last_page_len;
+  dp.hdr = (const int32_t*)(ws + L.hdr);
+  dp.work = (const int4*)(ws + L.work);
+  dp.chunk_indptr = (const int32_t*)(ws + L.chunk_indptr);
+  dp.lse_part = (float*)(ws + L.lse);
+  dp.o_part = (float*)(ws + L.opart);
+  dp.out = out;
+  dp.out_stride_tok = out_stride_token;
+  dp.out_stride_head = out_stride_head;
+  dp.num_kv_heads = nkv;
+  dp.group = num_qo_heads / nkv;
+  dp.page_size = kv->page_size;
+  dp.causal = causal ? 1 : 0;
+  dp.scale_log2 = sm_scale * 1.4426950408889634f;
+  const int grid = (int)((L.max_chunks * (int64_t)nkv + 3) / 4);
+  int st;
+  if (q_dtype == MI_BF16)
+    st = fp8 ? dispatch_d<BF16, true>(dp, D, grid, batch, phases, stream)
+             : dispatch_d<BF16, false>(dp, D, grid, batch, phases, stream);
+  else
+    st = fp8 ? dispatch_d<F16, true>(dp, D, grid, batch, phases, stream)
+             : dispatch_d<F16, false>(dp, D, grid, batch, phases, stream);
+  if (st != MI_OK) return st;
+  MI_CHECK_LAUNCH();
+  return MI_OK;
+}
+
+int64_t decode_workspace_bytes_impl(int32_t batch, int32_t num_kv_heads, int32_t head_dim) {
+  if (batch < 0 || num_kv_heads <= 0 || head_dim <= 0) return MI_ERR_INVALID;
+  return split_layout(batch, num_kv_heads, head_dim, -1).total;
+}
+
+}  // namespace mi
+
+extern "C" {
+
+int64_t mi_decode_workspace_bytes(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                  int32_t head_dim) {
+  if (num_qo_heads <= 0) return MI_ERR_INVALID;
+  return mi::decode_workspace_bytes_impl(batch, num_kv_heads, head_dim);
+}
+
+int mi_decode_plan(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                   const int32_t* last_page_len, int32_t batch, int32_t page_size,
+                   int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                   int64_t* kv_locations, void* workspace, int64_t workspace_bytes, void* stream) {
+  return mi::decode_plan_impl(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size,
+                              num_qo_heads, num_kv_heads, head_dim, kv_locations, workspace,
+                              workspace_bytes, 0, (hipStream_t)stream);
+}
+
+#define MI_DECODE_ARGS                                                                           \
+  const void *q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,                 \
+      const mi_paged_kv *kv, const int32_t *qo_indptr, const int32_t *kv_indptr,                 \
+      const int32_t *kv_indices, const int32_t *last_page_len, int32_t batch, int32_t num_qo_heads, \
+      int32_t causal, float sm_scale, void *workspace, int64_t workspace_bytes, void *out,       \
+      int64_t out_stride_token, int64_t out_stride_head, void *stream
+#define MI_DECODE_FWD(phases)                                                                      \
+  mi::decode_run_impl(q, q_dtype, q_stride_token, q_stride_head, kv, qo_indptr, kv_indptr,         \
+                      kv_indices, last_page_len, batch, num_qo_heads, causal, sm_scale, workspace, \
+                      workspace_bytes, 0, out, out_stride_token, out_stride_head, phases,          \
+                      (hipStream_t)stream)
+
+int mi_decode_run(MI_DECODE_ARGS) { return MI_DECODE_FWD(mi::kPhaseAttend | mi::kPhaseMerge); }
+int mi_decode_attend(MI_DECODE_ARGS) { return MI_DECODE_FWD(mi::kPhaseAttend); }
+int mi_decode_merge(MI_DECODE_ARGS) { return MI_DECODE_FWD(mi::kPhaseMerge); }
+
+}  // extern "C"

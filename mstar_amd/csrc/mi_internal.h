@@ -1,0 +1,59 @@
+// Internal interfaces shared between the decode and prefill translation units.
+#pragma once
+
+#include "mi_common.h"
+
+namespace mi {
+
+// Workspace layout of a split-KV plan (decode kernel + merge).
+struct SplitLayout {
+  int64_t hdr, chunk_indptr, work, lse, opart, total;
+  int32_t max_chunks;
+};
+// ws_avail: bytes the caller's workspace offers from the layout's start (-1:
+// unbounded, giving the recommended size); the chunk budget shrinks to fit.
+SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t ws_avail);
+
+int decode_plan_impl(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                     const int32_t* last_page_len, int32_t batch, int32_t page_size,
+                     int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int64_t* kv_locations, void* workspace, int64_t workspace_bytes,
+                     int64_t ws_offset, hipStream_t stream);
+
+enum : int { kPhaseAttend = 1, kPhaseMerge = 2 };
+
+int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                    const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                    const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                    int32_t num_qo_heads, int32_t causal, float sm_scale, void* workspace,
+                    int64_t workspace_bytes, int64_t ws_offset, void* out,
+                    int64_t out_stride_token, int64_t out_stride_head, int phases, hipStream_t stream);
+
+// Exclusive prefix sum over a 1024-thread block; `smem` holds >= 16 ints.
+__device__ __forceinline__ int block_exclusive_scan_1024(int v, int& total, int* smem) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) smem[w] = x;
+  __syncthreads();
+  if (w == 0) {
+    int t = lane < 16 ? smem[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int y = __shfl_up(t, o, 64);
+      if (lane >= o) t += y;
+    }
+    if (lane < 16) smem[lane] = t;
+  }
+  __syncthreads();
+  const int before = w ? smem[w - 1] : 0;
+  total = smem[15];
+  __syncthreads();
+  return before + x - v;
+}
+
+}  // namespace mi

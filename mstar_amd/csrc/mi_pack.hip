@@ -1,0 +1,140 @@
+// Per-step batch packing (P1) on the GPU.
+//
+// Replaces the per-request Python loop of
+// BatchedCacheManager._plan_attention_impl (mstar/engine/cache_manager.py:272-322)
+// and its host->device copies.  Page ids stay owned by the host FIFO
+// allocator (mstar/engine/kv_store.py:25-67, 463-482); each newly allocated
+// page is written once into a device block table (mi_block_table_update),
+// and this kernel flattens the batch from that table every step.
+//
+// Every workgroup recomputes the two exclusive prefix sums (new tokens and
+// pages per request) in LDS, so the grid needs no inter-block
+// synchronisation; the flattening of kv_indices is then shared by all
+// workgroups (grid-stride over the batch's pages, one binary search in LDS
+// per page id).
+#include "mi_common.h"
+#include "mi_internal.h"
+
+namespace mi {
+
+constexpr int kPackThreads = 1024;
+
+struct PackParams {
+  const int32_t* req_slot;
+  const int32_t* seq_len;
+  const int32_t* new_len;
+  const int32_t* num_pages;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int32_t* qo_indptr;
+  int32_t* kv_indptr;
+  int32_t* kv_indices;
+  int32_t* last_page_len;
+  int64_t* kv_locations;
+  int32_t batch, page_size;
+};
+
+__global__ __launch_bounds__(kPackThreads) void pack_kernel(PackParams p) {
+  __shared__ int s_scan[16];
+  __shared__ int s_off[kPackThreads + 1];  // window-relative exclusive page offsets
+  __shared__ int s_slot[kPackThreads];
+  const int tid = threadIdx.x;
+  int carry_qo = 0, carry_kv = 0;
+  for (int base = 0; base < p.batch; base += kPackThreads) {
+    const int b = base + tid;
+    const bool live = b < p.batch;
+    const int sl = live ? p.new_len[b] : 0;
+    const int np = live ? p.num_pages[b] : 0;
+    int tot_qo, tot_kv;
+    const int ex_qo = block_exclusive_scan_1024(sl, tot_qo, s_scan);
+    const int ex_kv = block_exclusive_scan_1024(np, tot_kv, s_scan);
+    s_off[tid] = ex_kv;
+    s_slot[tid] = live ? p.req_slot[b] : 0;
+    if (tid == 0) s_off[kPackThreads] = tot_kv;
+    if (blockIdx.x == 0 && live) {
+      p.qo_indptr[b] = carry_qo + ex_qo;
+      p.kv_indptr[b] = carry_kv + ex_kv;
+      const int T = p.seq_len[b] + sl;
+      int lpl = T % p.page_size;
+      if (lpl == 0) lpl = p.page_size;
+      p.last_page_len[b] = lpl;
+      if (p.kv_locations && sl == 1) {
+        // (last page of the request's list, last_page_len - 1): cache_manager.py:293-294
+        int64_t page = -1, pos = -1;
+        if (np > 0) {
+          page = p.block_table[(int64_t)s_slot[tid] * p.bt_stride + (np - 1)];
+          pos = lpl - 1;
+        }
+        p.kv_locations[2 * b] = page;
+        p.kv_locations[2 * b + 1] = pos;
+      }
+    }
+    __syncthreads();
+    // flatten this window's page lists: kv_indices[carry_kv + f] for f < tot_kv
+    const int nreq = min(kPackThreads, p.batch - base);
+    for (int f = blockIdx.x * kPackThreads + tid; f < tot_kv; f += gridDim.x * kPackThreads) {
+      int lo = 0, hi = nreq - 1;  // last r with s_off[r] <= f
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_off[mid] <= f) lo = mid; else hi = mid - 1;
+      }
+      p.kv_indices[carry_kv + f] = p.block_table[(int64_t)s_slot[lo] * p.bt_stride + (f - s_off[lo])];
+    }
+    carry_qo += tot_qo;
+    carry_kv += tot_kv;
+    __syncthreads();
+  }
+  if (blockIdx.x == 0 && tid == 0) {
+    p.qo_indptr[p.batch] = carry_qo;
+    p.kv_indptr[p.batch] = carry_kv;
+  }
+}
+
+__global__ __launch_bounds__(256) void block_table_update_kernel(int32_t* table, int64_t stride,
+                                                                 const int32_t* slot, const int32_t* pos,
+                                                                 const int32_t* page, int32_t n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) table[(int64_t)slot[i] * stride + pos[i]] = page[i];
+}
+
+}  // namespace mi
+
+extern "C" int mi_pack(const int32_t* req_slot, const int32_t* seq_len, const int32_t* new_len,
+                       const int32_t* num_pages, int32_t batch, const int32_t* block_table,
+                       int64_t block_table_stride, int32_t page_size, int32_t* qo_indptr,
+                       int32_t* kv_indptr, int32_t* kv_indices, int32_t* last_page_len,
+                       int64_t* kv_locations, int32_t grid_blocks, void* stream) {
+  using namespace mi;
+  if (batch < 0 || page_size <= 0 || grid_blocks <= 0 || block_table_stride <= 0) return MI_ERR_INVALID;
+  if (!qo_indptr || !kv_indptr || !last_page_len) return MI_ERR_INVALID;
+  if (batch > 0 && (!req_slot || !seq_len || !new_len || !num_pages || !block_table || !kv_indices))
+    return MI_ERR_INVALID;
+  PackParams pp;
+  pp.req_slot = req_slot;
+  pp.seq_len = seq_len;
+  pp.new_len = new_len;
+  pp.num_pages = num_pages;
+  pp.block_table = block_table;
+  pp.bt_stride = block_table_stride;
+  pp.qo_indptr = qo_indptr;
+  pp.kv_indptr = kv_indptr;
+  pp.kv_indices = kv_indices;
+  pp.last_page_len = last_page_len;
+  pp.kv_locations = kv_locations;
+  pp.batch = batch;
+  pp.page_size = page_size;
+  hipLaunchKernelGGL(pack_kernel, dim3(grid_blocks), dim3(kPackThreads), 0, (hipStream_t)stream, pp);
+  MI_CHECK_LAUNCH();
+  return MI_OK;
+}
+
+extern "C" int mi_block_table_update(int32_t* block_table, int64_t stride, const int32_t* slot,
+                                     const int32_t* pos, const int32_t* page, int32_t n, void* stream) {
+  if (n < 0 || stride <= 0) return MI_ERR_INVALID;
+  if (n == 0) return MI_OK;
+  if (!block_table || !slot || !pos || !page) return MI_ERR_INVALID;
+  hipLaunchKernelGGL(mi::block_table_update_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                     (hipStream_t)stream, block_table, stride, slot, pos, page, n);
+  MI_CHECK_LAUNCH();
+  return MI_OK;
+}

@@ -1,0 +1,460 @@
+"""plan()/run()/set_kv_cache() wrappers over the gfx950 kernels.
+
+Drop-in replacements for M*'s ``FlashInferPrefillWrapper`` and
+``FlashInferDecodeWrapper`` (``mstar/utils/flashinfer_utils.py:70-484``): same
+constructor arguments, same ``plan``/``run``/``set_kv_cache`` signatures and the
+same attributes that M*'s cache manager and CUDA-graph runner read
+(``_qo_indptr_buf``, ``token_to_page``, ``token_to_cache``, ``_total_tokens``,
+``kv_cache_locations``, ``_n_req``, the ``_paged_kv_*_buf`` static buffers).
+The reference names are exported as aliases.
+
+KV layer layout: ``[max_pages, 2, page_size, num_kv_heads, head_dim]`` (NHD).
+
+Differences from the reference, all deliberate:
+
+* No FlashInfer: planning runs on the GPU (``mi_decode_plan`` /
+  ``mi_prefill_plan``) and never reads device memory back on the host.
+  ``plan()`` accepts CPU or device index tensors; CPU tensors go through one
+  pinned, asynchronous host->device copy.
+* ``set_kv_cache`` writes K and V in one kernel and, in CUDA-graph mode, skips
+  the padding tokens beyond the planned count (the reference maps them to
+  page 0 slot 0, ``flashinfer_utils.py:251-253``).
+* Optional fp8-e4m3 KV caches (``torch.float8_e4m3fn``) with per-head fp32
+  ``k_scale``/``v_scale`` passed to ``set_kv_cache`` and ``run``.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "PagedPrefillWrapper",
+    "PagedDecodeWrapper",
+    "FlashInferPrefillWrapper",
+    "FlashInferDecodeWrapper",
+]
+
+_MAX_GROUP = 16  # q heads per kv head handled by one MFMA tile
+
+
+def _check_heads(num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int) -> None:
+    if num_kv_heads <= 0 or num_qo_heads % num_kv_heads:
+        raise ValueError(f"num_qo_heads={num_qo_heads} must be a multiple of num_kv_heads={num_kv_heads}")
+    if num_qo_heads // num_kv_heads > _MAX_GROUP:
+        raise ValueError(f"GQA group {num_qo_heads // num_kv_heads} > {_MAX_GROUP} is not supported")
+    if head_dim not in (64, 128, 256):
+        raise ValueError(f"head_dim {head_dim} not supported (64, 128, 256)")
+    if page_size <= 0 or page_size % 16:
+        raise ValueError(f"page_size {page_size} must be a positive multiple of 16")
+
+
+class _Staging:
+    """Pinned host buffer for asynchronous index uploads, reused across plans."""
+
+    def __init__(self):
+        self.buf: torch.Tensor | None = None
+        self.event: torch.cuda.Event | None = None
+
+    def upload(self, parts: list[torch.Tensor], device: torch.device,
+               dests: list[torch.Tensor | None]) -> list[torch.Tensor]:
+        """Copy CPU int tensors to the device in one transfer.
+
+        ``dests[i]`` (a device tensor of at least ``parts[i].numel()``
+        elements, same dtype) receives part ``i`` in place; ``None`` allocates.
+        """
+        flat = [p.reshape(-1).view(torch.int32) if p.dtype == torch.int64 else p.reshape(-1) for p in parts]
+        sizes = [f.numel() for f in flat]
+        total = sum(sizes)
+        if self.buf is None or self.buf.numel() < total:
+            self.buf = torch.empty(max(total, 1 << 16), dtype=torch.int32, pin_memory=True)
+            self.event = None
+        if self.event is not None:
+            self.event.synchronize()
+        off = 0
+        for f, n in zip(flat, sizes):
+            self.buf[off:off + n].copy_(f)
+            off += n
+        staged = torch.empty(total, dtype=torch.int32, device=device)
+        staged.copy_(self.buf[:total], non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record()
+        outs = []
+        off = 0
+        for p, f, n, d in zip(parts, flat, sizes, dests):
+            piece = staged[off:off + n]
+            if p.dtype == torch.int64:
+                piece = piece.view(torch.int64)
+            piece = piece.view(p.shape)
+            off += n
+            if d is not None:
+                d.view(-1)[: piece.numel()].copy_(piece.reshape(-1))
+                outs.append(d)
+            else:
+                outs.append(piece)
+        return outs
+
+
+def _as_device_int(t: torch.Tensor, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    if t.device != device:
+        t = t.to(device, non_blocking=True)
+    return t.contiguous()
+
+
+def _q_strides(q: torch.Tensor, name: str) -> tuple[int, int]:
+    if q.dim() != 3 or q.stride(2) != 1:
+        raise ValueError(f"{name} must be [tokens, heads, head_dim] with contiguous head_dim")
+    if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+        raise ValueError(f"{name}: rows must be 16-byte aligned")
+    return q.stride(0), q.stride(1)
+
+
+def _kv_src(k: torch.Tensor, name: str) -> torch.Tensor:
+    if k.dim() != 3:
+        raise ValueError(f"{name} must be [tokens, num_kv_heads, head_dim]")
+    if k.stride(2) != 1 or k.stride(0) % 8 or k.stride(1) % 8 or k.data_ptr() % (8 * k.element_size()):
+        k = k.contiguous()
+    return k
+
+
+def _append(kv_cache_layer: torch.Tensor, k: torch.Tensor, v: torch.Tensor, page_idx: torch.Tensor,
+            slot_idx_ptr: int, idx_stride: int, n: int, n_dev_ptr: int | None,
+            k_scale: torch.Tensor | None, v_scale: torch.Tensor | None) -> None:
+    if n == 0:
+        return
+    desc = _lib.paged_kv_desc(kv_cache_layer, k_scale, v_scale)
+    if k.shape[1:] != (desc.num_kv_heads, desc.head_dim) or v.shape[1:] != k.shape[1:]:
+        raise ValueError(f"k/v shape {tuple(k.shape)} does not match the cache heads/head_dim")
+    if k.shape[0] < n or v.shape[0] < n:
+        raise ValueError(f"k/v hold {k.shape[0]} tokens, {n} planned")
+    src_dt = _lib.TORCH_TO_MI.get(k.dtype)
+    if src_dt is None or src_dt == _lib.MI_FP8_E4M3:
+        raise ValueError(f"unsupported k/v dtype {k.dtype}")
+    if v.dtype != k.dtype:
+        v = v.to(k.dtype)
+    k = _kv_src(k, "k")
+    v = _kv_src(v, "v")
+    _lib.check(
+        _lib.lib().mi_kv_append(
+            desc, k.data_ptr(), v.data_ptr(), src_dt, k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+            page_idx.data_ptr(), slot_idx_ptr, idx_stride, n, n_dev_ptr, _lib.stream_ptr(kv_cache_layer.device),
+        ),
+        "mi_kv_append",
+    )
+
+
+class PagedDecodeWrapper:
+    """Batched paged decode attention (``flashinfer_utils.py:291-484``)."""
+
+    def __init__(
+        self,
+        workspace_buffer: torch.Tensor,
+        num_qo_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        page_size: int,
+        batch_size: int | None = None,
+        max_num_pages: int | None = None,
+        device: torch.device = torch.device("cuda"),
+        use_cuda_graph: bool = False,
+        enable_nvtx: bool = False,
+    ):
+        _check_heads(num_qo_heads, num_kv_heads, head_dim, page_size)
+        _lib.lib()
+        self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.use_cuda_graph = use_cuda_graph
+        self.enable_nvtx = enable_nvtx
+        self.batch_size = batch_size
+        self.num_qo_heads = num_qo_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.page_size = page_size
+        self.dtype = None
+        self._workspace = workspace_buffer
+        self._staging = _Staging()
+        self._n_req = 0
+        if use_cuda_graph:
+            assert batch_size is not None, "batch_size required for CUDA graph mode"
+            assert max_num_pages is not None, "max_num_pages required for CUDA graph mode"
+            self._paged_kv_indptr_buf = torch.zeros(batch_size + 1, dtype=torch.int32, device=self.device)
+            self._paged_kv_indices_buf = torch.zeros(max_num_pages, dtype=torch.int32, device=self.device)
+            self._paged_kv_last_page_len_buf = torch.ones(batch_size, dtype=torch.int32, device=self.device)
+            self.kv_cache_locations = torch.zeros(batch_size, 2, dtype=torch.long, device=self.device)
+        else:
+            self.kv_cache_locations = None
+
+    # -------------------------------------------------------------- plan
+    def plan(
+        self,
+        paged_kv_indptr: torch.Tensor,
+        paged_kv_indices: torch.Tensor,
+        paged_kv_last_page_len: torch.Tensor,
+        kv_cache_locations: torch.Tensor | None = None,
+        dtype: torch.dtype = torch.bfloat16,
+    ) -> None:
+        """Build the split-KV plan on the GPU (``flashinfer_utils.py:369-453``)."""
+        n_req = paged_kv_indptr.shape[0] - 1
+        if paged_kv_last_page_len.shape[0] != n_req:
+            raise ValueError("paged_kv_last_page_len must have one entry per request")
+        dev = self.device
+        if self.use_cuda_graph:
+            if n_req != self.batch_size:  # captured launches bake the batch in
+                raise ValueError(f"CUDA-graph mode plans a fixed batch of {self.batch_size}, got {n_req}")
+            if paged_kv_indices.shape[0] > self._paged_kv_indices_buf.shape[0]:
+                raise ValueError("paged_kv_indices exceeds max_num_pages")
+            dests = [self._paged_kv_indptr_buf, self._paged_kv_indices_buf, self._paged_kv_last_page_len_buf]
+        else:
+            dests = [None, None, None]
+        srcs = [paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len]
+        if all(t.device.type == "cpu" for t in srcs):
+            srcs = [t.to(torch.int32) for t in srcs]
+            indptr, indices, last = self._staging.upload(srcs, dev, dests)
+        else:
+            indptr, indices, last = [_as_device_int(t, torch.int32, dev) for t in srcs]
+            if self.use_cuda_graph:
+                for d, s in zip(dests, (indptr, indices, last)):
+                    if d.data_ptr() != s.data_ptr():
+                        d[: s.shape[0]].copy_(s)
+                indptr, indices, last = dests
+
+        if kv_cache_locations is not None:
+            loc = kv_cache_locations.to(dev, torch.long, non_blocking=True)
+            if self.use_cuda_graph:
+                self.kv_cache_locations[:n_req].copy_(loc)
+            else:
+                self.kv_cache_locations = loc
+            loc_out = None
+        else:
+            if not self.use_cuda_graph:
+                self.kv_cache_locations = torch.empty(n_req, 2, dtype=torch.long, device=dev)
+            loc_out = self.kv_cache_locations
+        _lib.check(
+            _lib.lib().mi_decode_plan(
+                None, indptr.data_ptr(), indices.data_ptr(), last.data_ptr(), n_req, self.page_size,
+                self.num_qo_heads, self.num_kv_heads, self.head_dim,
+                loc_out.data_ptr() if loc_out is not None else None,
+                self._workspace.data_ptr(), self._workspace.numel() * self._workspace.element_size(),
+                _lib.stream_ptr(dev),
+            ),
+            "mi_decode_plan",
+        )
+        self._indptr, self._indices, self._last = indptr, indices, last
+        self._n_req = n_req
+        self.dtype = dtype
+
+    # --------------------------------------------------------------- run
+    def run(self, q: torch.Tensor, kv_cache_layer: torch.Tensor, k_scale: torch.Tensor | None = None,
+            v_scale: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Paged decode attention (``flashinfer_utils.py:455-465``): q ``[n_req, Hq, D]`` -> o."""
+        if self.dtype is None:
+            raise RuntimeError("plan() must be called before run()")
+        q = q.to(self.dtype)
+        n = self._n_req
+        if q.dim() != 3 or q.shape[0] < n or q.shape[1] != self.num_qo_heads or q.shape[2] != self.head_dim:
+            raise ValueError(f"q shape {tuple(q.shape)} does not match the plan")
+        if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+            q = q.contiguous()
+        desc = _lib.paged_kv_desc(kv_cache_layer, k_scale, v_scale)
+        if desc.num_kv_heads != self.num_kv_heads or desc.head_dim != self.head_dim or desc.page_size != self.page_size:
+            raise ValueError("kv_cache_layer geometry does not match the wrapper")
+        if out is None:
+            out = torch.empty(q.shape[0], self.num_qo_heads, self.head_dim, dtype=q.dtype, device=q.device)
+        qs = _q_strides(q, "q")
+        os_ = _q_strides(out, "out")
+        batch = n
+        _lib.check(
+            _lib.lib().mi_decode_run(
+                q.data_ptr(), _lib.TORCH_TO_MI[q.dtype], qs[0], qs[1], desc, None, self._indptr.data_ptr(),
+                self._indices.data_ptr(), self._last.data_ptr(), batch, self.num_qo_heads, 0,
+                1.0 / math.sqrt(self.head_dim), self._workspace.data_ptr(),
+                self._workspace.numel() * self._workspace.element_size(), out.data_ptr(), os_[0], os_[1],
+                _lib.stream_ptr(q.device),
+            ),
+            "mi_decode_run",
+        )
+        return out
+
+    def set_kv_cache(self, kv_cache_layer: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None) -> None:
+        """Write one new token per request (``flashinfer_utils.py:467-484``)."""
+        n = self._n_req
+        loc = self.kv_cache_locations
+        _append(kv_cache_layer, k, v, loc, loc.data_ptr() + 8, 2, n, None, k_scale, v_scale)
+
+
+class PagedPrefillWrapper:
+    """Batched ragged paged prefill attention (``flashinfer_utils.py:70-288``)."""
+
+    def __init__(
+        self,
+        workspace_buffer: torch.Tensor,
+        num_qo_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        page_size: int,
+        batch_size: int | None = None,
+        max_total_tokens: int | None = None,
+        max_num_pages: int | None = None,
+        device: torch.device = torch.device("cuda"),
+        use_cuda_graph: bool = False,
+        enable_nvtx: bool = False,
+    ):
+        _check_heads(num_qo_heads, num_kv_heads, head_dim, page_size)
+        _lib.lib()
+        self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.use_cuda_graph = use_cuda_graph
+        self.enable_nvtx = enable_nvtx
+        self.batch_size = batch_size
+        self.max_total_tokens = max_total_tokens
+        self.num_qo_heads = num_qo_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.page_size = page_size
+        self.dtype = None
+        self.causal = True
+        self._workspace = workspace_buffer
+        self._staging = _Staging()
+        self._n_req = 0
+        if use_cuda_graph:
+            assert batch_size is not None, "batch_size required for CUDA graph mode"
+            assert max_total_tokens is not None, "max_total_tokens required for CUDA graph mode"
+            assert max_num_pages is not None, "max_num_pages required for CUDA graph mode"
+            d = self.device
+            self._qo_indptr_buf = torch.zeros(batch_size + 1, dtype=torch.int32, device=d)
+            self._paged_kv_indptr_buf = torch.zeros(batch_size + 1, dtype=torch.int32, device=d)
+            self._paged_kv_indices_buf = torch.zeros(max_num_pages, dtype=torch.int32, device=d)
+            self._paged_kv_last_page_len_buf = torch.ones(batch_size, dtype=torch.int32, device=d)
+            self.token_to_page = torch.zeros(max_total_tokens, dtype=torch.long, device=d)
+            self.token_to_cache = torch.zeros(max_total_tokens, dtype=torch.long, device=d)
+        else:
+            self.token_to_page = None
+            self.token_to_cache = None
+        self._total_tokens = 0
+
+    def plan(
+        self,
+        qo_indptr: torch.Tensor,
+        paged_kv_indptr: torch.Tensor,
+        paged_kv_indices: torch.Tensor,
+        paged_kv_last_page_len: torch.Tensor,
+        causal: bool = True,
+        dtype: torch.dtype = torch.bfloat16,
+    ) -> None:
+        """Token->page map and work partition on the GPU (``flashinfer_utils.py:162-256``).
+
+        ``_total_tokens`` is read from ``qo_indptr[-1]``: free for CPU inputs,
+        one device sync for device inputs (as the reference, ``:215``).
+        """
+        srcs = [qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len]
+        on_cpu = all(t.device.type == "cpu" for t in srcs)
+        total_tokens = int(qo_indptr[-1]) if on_cpu else int(qo_indptr[-1].item())
+        self._plan(qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len, total_tokens, causal, dtype)
+
+    def plan_device(self, qo_indptr: torch.Tensor, paged_kv_indptr: torch.Tensor, paged_kv_indices: torch.Tensor,
+                    paged_kv_last_page_len: torch.Tensor, total_tokens: int, causal: bool = True,
+                    dtype: torch.dtype = torch.bfloat16) -> None:
+        """:meth:`plan` for device index tensors whose token count the caller knows (no sync)."""
+        self._plan(qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len, total_tokens, causal, dtype)
+
+    def _plan(self, qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len, total_tokens, causal,
+              dtype) -> None:
+        n_req = qo_indptr.shape[0] - 1
+        if paged_kv_indptr.shape[0] != n_req + 1 or paged_kv_last_page_len.shape[0] != n_req:
+            raise ValueError("index tensors disagree on the number of requests")
+        dev = self.device
+        self.dtype = dtype
+        self.causal = bool(causal)
+        srcs = [qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len]
+        on_cpu = all(t.device.type == "cpu" for t in srcs)
+        self._total_tokens = total_tokens
+        if self.use_cuda_graph:
+            if n_req != self.batch_size:  # captured launches bake the batch in
+                raise ValueError(f"CUDA-graph mode plans a fixed batch of {self.batch_size}, got {n_req}")
+            if total_tokens > self.max_total_tokens:
+                raise ValueError(f"{total_tokens} tokens > max_total_tokens {self.max_total_tokens}")
+            if paged_kv_indices.shape[0] > self._paged_kv_indices_buf.shape[0]:
+                raise ValueError("paged_kv_indices exceeds max_num_pages")
+            dests = [self._qo_indptr_buf, self._paged_kv_indptr_buf, self._paged_kv_indices_buf,
+                     self._paged_kv_last_page_len_buf]
+        else:
+            dests = [None] * 4
+        if on_cpu:
+            qo, indptr, indices, last = self._staging.upload([t.to(torch.int32) for t in srcs], dev, dests)
+        else:
+            qo, indptr, indices, last = [_as_device_int(t, torch.int32, dev) for t in srcs]
+            if self.use_cuda_graph:
+                for d, s in zip(dests, (qo, indptr, indices, last)):
+                    if d.data_ptr() != s.data_ptr():
+                        d[: s.shape[0]].copy_(s)
+                qo, indptr, indices, last = dests
+        if not self.use_cuda_graph:
+            self._qo_indptr_buf = qo
+            self.token_to_page = torch.empty(total_tokens, dtype=torch.long, device=dev)
+            self.token_to_cache = torch.empty(total_tokens, dtype=torch.long, device=dev)
+        batch = n_req
+        max_tokens = self.max_total_tokens if self.use_cuda_graph else total_tokens
+        ws_bytes = self._workspace.numel() * self._workspace.element_size()
+        _lib.check(
+            _lib.lib().mi_prefill_plan(
+                qo.data_ptr(), indptr.data_ptr(), indices.data_ptr(), last.data_ptr(), n_req, max_tokens,
+                self.page_size, self.num_qo_heads, self.num_kv_heads, self.head_dim,
+                self.token_to_page.data_ptr(), self.token_to_cache.data_ptr(), self.token_to_page.shape[0],
+                self._workspace.data_ptr(), ws_bytes, _lib.stream_ptr(dev),
+            ),
+            "mi_prefill_plan",
+        )
+        self._qo, self._indptr, self._indices, self._last = qo, indptr, indices, last
+        self._n_req = n_req
+        self._plan_batch = batch
+        self._plan_max_tokens = max_tokens
+
+    def run(self, q: torch.Tensor, kv_cache_layer: torch.Tensor, k_scale: torch.Tensor | None = None,
+            v_scale: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Ragged paged attention (``flashinfer_utils.py:258-269``): q ``[tokens, Hq, D]`` -> o."""
+        if self.dtype is None:
+            raise RuntimeError("plan() must be called before run()")
+        q = q.to(self.dtype)
+        if q.dim() != 3 or q.shape[1] != self.num_qo_heads or q.shape[2] != self.head_dim:
+            raise ValueError(f"q shape {tuple(q.shape)} does not match the wrapper")
+        if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+            q = q.contiguous()
+        desc = _lib.paged_kv_desc(kv_cache_layer, k_scale, v_scale)
+        if desc.num_kv_heads != self.num_kv_heads or desc.head_dim != self.head_dim or desc.page_size != self.page_size:
+            raise ValueError("kv_cache_layer geometry does not match the wrapper")
+        if out is None:
+            out = torch.empty(q.shape[0], self.num_qo_heads, self.head_dim, dtype=q.dtype, device=q.device)
+        qs = _q_strides(q, "q")
+        os_ = _q_strides(out, "out")
+        ws_bytes = self._workspace.numel() * self._workspace.element_size()
+        _lib.check(
+            _lib.lib().mi_prefill_run(
+                q.data_ptr(), _lib.TORCH_TO_MI[q.dtype], qs[0], qs[1], desc, self._qo.data_ptr(),
+                self._indptr.data_ptr(), self._indices.data_ptr(), self._last.data_ptr(), self._plan_batch,
+                self._plan_max_tokens, self.num_qo_heads, 1 if self.causal else 0, 1.0 / math.sqrt(self.head_dim),
+                self._workspace.data_ptr(), ws_bytes, out.data_ptr(), os_[0], os_[1], _lib.stream_ptr(q.device),
+            ),
+            "mi_prefill_run",
+        )
+        return out
+
+    def set_kv_cache(self, kv_cache_layer: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None) -> None:
+        """Scatter the planned tokens' K/V into their pages (``flashinfer_utils.py:271-288``)."""
+        n = self._total_tokens
+        n_dev = self._qo.data_ptr() + 4 * self._n_req  # qo_indptr[n_req]: real count on the device
+        _append(kv_cache_layer, k, v, self.token_to_page, self.token_to_cache.data_ptr(), 1, n, n_dev,
+                k_scale, v_scale)
+
+
+# Reference names (mstar/utils/flashinfer_utils.py) for drop-in use.
+FlashInferPrefillWrapper = PagedPrefillWrapper
+FlashInferDecodeWrapper = PagedDecodeWrapper

@@ -1,0 +1,135 @@
+"""GPU parity: decode wrapper (plan -> set_kv_cache -> run) against the CPU oracle.
+
+Tolerance: max-abs 2e-2 for bf16/fp16 KV and 6e-2 for fp8-e4m3 KV against
+fp32 attention over the same (dequantised) cache — the north-star bar.
+The appended cache must equal the oracle's append bit for bit.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import A, P, S, custom_batch, decode_reference, log, max_abs, random_cache, workspace
+from mstar_amd.paged_attention import FlashInferDecodeWrapper
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16 = 2e-2
+TOL_FP8 = 6e-2
+
+
+def _run_decode(gpu, hq, hkv, d, ps, kv_indptr, kv_indices, last, pool, seed, dtype=torch.bfloat16,
+                fp8=False, cpu_index=True):
+    b = len(last)
+    g = torch.Generator().manual_seed(seed + 1000)
+    cache_src = random_cache(pool, ps, hkv, d, seed, torch.float32)
+    q = torch.randn(b, hq, d, generator=g).to(dtype)
+    k_new = torch.randn(b, hkv, d, generator=g).to(dtype)
+    v_new = torch.randn(b, hkv, d, generator=g).to(dtype)
+    if fp8:
+        ks = A.head_scales(cache_src[:, 0].reshape(-1, hkv, d))
+        vs = A.head_scales(cache_src[:, 1].reshape(-1, hkv, d))
+        cache_cpu = torch.empty(pool, 2, ps, hkv, d, dtype=torch.float8_e4m3fn)
+        cache_cpu[:, 0] = A.quantize_e4m3(cache_src[:, 0].reshape(-1, hkv, d), ks).view(pool, ps, hkv, d)
+        cache_cpu[:, 1] = A.quantize_e4m3(cache_src[:, 1].reshape(-1, hkv, d), vs).view(pool, ps, hkv, d)
+        scales = (ks.to(gpu), vs.to(gpu))
+    else:
+        ks = vs = None
+        cache_cpu = cache_src.to(dtype)
+        scales = (None, None)
+    cache = cache_cpu.to(gpu)
+    # oracle: append then attend
+    loc = P.decode_locations(kv_indptr, kv_indices, last)
+    A.append(cache_cpu, loc[:, 0], loc[:, 1], k_new, v_new, ks, vs)
+    ref = decode_reference(q, cache_cpu, kv_indptr, kv_indices, last, ks, vs)
+
+    wrapper = FlashInferDecodeWrapper(workspace(gpu), hq, hkv, d, ps, device=gpu)
+    t = (lambda x: torch.as_tensor(x)) if cpu_index else (lambda x: torch.as_tensor(x).to(gpu))
+    wrapper.plan(t(kv_indptr), t(kv_indices), t(last), dtype=dtype)
+    wrapper.set_kv_cache(cache, k_new.to(gpu), v_new.to(gpu), *scales)
+    out = wrapper.run(q.to(gpu), cache, *scales)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.cpu().view(torch.uint8), cache_cpu.view(torch.uint8)), "append is not bit-exact"
+    assert torch.equal(wrapper.kv_cache_locations.cpu(), torch.as_tensor(loc)), "write locations differ"
+    return out, ref
+
+
+@pytest.mark.parametrize("name,nreq", [("c1", None), ("c2", 16), ("c3", 6)])
+def test_decode_configs(gpu, name, nreq):
+    bt = S.make_batch(name, batch=nreq)
+    s = bt.spec
+    idx, pool = (bt.kv_indices, s.pool_pages) if s.pool_pages <= 4096 else _compact(bt)
+    log(f"decode {name} B={len(bt.kv_len)} pages={bt.total_pages} pool={pool}")
+    out, ref = _run_decode(gpu, s.num_qo_heads, s.num_kv_heads, s.head_dim, s.page_size, bt.kv_indptr,
+                           idx, bt.last_page_len, pool, s.seed)
+    err = max_abs(out, ref)
+    log(f"  max_abs={err:.3e}")
+    assert err < TOL_BF16
+
+
+def _compact(bt):
+    """Renumber a batch's pages into a pool just large enough (keeps CPU memory small)."""
+    uniq = np.unique(bt.kv_indices)
+    remap = np.searchsorted(uniq, bt.kv_indices).astype(np.int32)
+    rng = np.random.default_rng(0)
+    perm = rng.permutation(len(uniq)).astype(np.int32)
+    return perm[remap], len(uniq)
+
+
+@pytest.mark.parametrize("name,nreq", [("c3", 6), ("c5", 6)])
+def test_decode_long_context_split(gpu, name, nreq):
+    bt = S.make_batch(name, batch=nreq)
+    s = bt.spec
+    idx, pool = _compact(bt)
+    log(f"decode-long {name} B={nreq} max_T={bt.kv_len.max()} pool={pool}")
+    out, ref = _run_decode(gpu, s.num_qo_heads, s.num_kv_heads, s.head_dim, s.page_size, bt.kv_indptr, idx,
+                           bt.last_page_len, pool, s.seed, fp8=(s.kv_dtype == "fp8"))
+    err = max_abs(out, ref)
+    log(f"  max_abs={err:.3e}")
+    assert err < (TOL_FP8 if s.kv_dtype == "fp8" else TOL_BF16)
+
+
+@pytest.mark.parametrize(
+    "hq,hkv,d,ps",
+    [(8, 1, 256, 16), (8, 2, 64, 16), (24, 8, 128, 32), (28, 4, 128, 16), (16, 1, 128, 128), (4, 4, 128, 16),
+     (32, 2, 64, 64)],
+)
+def test_decode_shapes(gpu, hq, hkv, d, ps):
+    lens = [1, 15, 16, 17, 255, 256, 257, 1000, 3001]
+    qo, kv_indptr, kv_indices, last = custom_batch(lens, ps, 600, seed=hq + d + ps)
+    log(f"decode-shape hq={hq} hkv={hkv} d={d} ps={ps}")
+    out, ref = _run_decode(gpu, hq, hkv, d, ps, kv_indptr, kv_indices, last, 600, seed=7)
+    err = max_abs(out, ref)
+    log(f"  max_abs={err:.3e}")
+    assert err < TOL_BF16
+
+
+def test_decode_fp16_and_device_indices(gpu):
+    qo, kv_indptr, kv_indices, last = custom_batch([5, 70, 700], 16, 64, seed=3)
+    out, ref = _run_decode(gpu, 8, 2, 128, 16, kv_indptr, kv_indices, last, 64, seed=3, dtype=torch.float16,
+                           cpu_index=False)
+    assert out.dtype == torch.float16
+    assert max_abs(out, ref) < TOL_BF16
+
+
+def test_decode_fp8_shapes(gpu):
+    qo, kv_indptr, kv_indices, last = custom_batch([1, 17, 400, 5000], 16, 400, seed=11)
+    for hq, hkv, d in [(32, 4, 128), (8, 1, 256), (8, 2, 64)]:
+        out, ref = _run_decode(gpu, hq, hkv, d, 16, kv_indptr, kv_indices, last, 400, seed=11, fp8=True)
+        err = max_abs(out, ref)
+        log(f"decode-fp8 hq={hq} hkv={hkv} d={d} max_abs={err:.3e}")
+        assert err < TOL_FP8
+
+
+def test_decode_is_deterministic(gpu):
+    qo, kv_indptr, kv_indices, last = custom_batch([3000, 20, 9000], 16, 1024, seed=5)
+    cache = random_cache(1024, 16, 4, 128, 5).to(gpu)
+    q = torch.randn(3, 32, 128, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(gpu)
+    w = FlashInferDecodeWrapper(workspace(gpu), 32, 4, 128, 16, device=gpu)
+    w.plan(torch.as_tensor(kv_indptr), torch.as_tensor(kv_indices), torch.as_tensor(last))
+    a = w.run(q, cache)
+    b = w.run(q, cache)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

@@ -1,0 +1,133 @@
+"""GPU parity: packing (mi_pack via BatchedCacheManager) and the decode plan are bit-exact.
+
+Multi-step scenarios drive our host allocator and the oracle's FIFO restatement
+side by side (prefill, decode steps, request removal with page reuse), and
+compare every packed tensor the GPU produces with the oracle's.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import P, log, workspace
+from mstar_amd import _lib
+from mstar_amd.cache_manager import BatchedCacheManager, WorkspaceBufferManager
+from mstar_amd.kv_store import AllocationFailedError, KVCacheConfig, PagedAllocationManager
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(gpu, max_pages, ps=16, hq=8, hkv=2, d=128, max_seq_len=8192):
+    cfg = KVCacheConfig(num_layers=1, num_kv_heads=hkv, head_dim=d, max_seq_len=max_seq_len,
+                        max_num_pages=max_pages, page_size=ps, num_qo_heads=hq)
+    kv = torch.zeros(1, max_pages, 2, ps, hkv, d, dtype=torch.bfloat16, device=gpu)
+    mgr = PagedAllocationManager(cfg, kv, device=gpu)
+    return cfg, kv, mgr
+
+
+def _check_step(cm, rids, label, seq_lens, ostates, opool, ps):
+    cm.plan_attention(seq_lens, label=label)
+    ref = P.pack(ostates, seq_lens, opool, ps)
+    qo, kv_indptr, kv_indices, last, loc = cm._last_pack
+    torch.cuda.synchronize()
+    assert qo.cpu().numpy().tolist() == ref.qo_indptr.tolist()
+    assert kv_indptr.cpu().numpy().tolist() == ref.kv_indptr.tolist()
+    assert kv_indices.cpu().numpy().tolist() == ref.kv_indices.tolist()
+    assert last.cpu().numpy().tolist() == ref.last_page_len.tolist()
+    if ref.kv_locations is not None:
+        assert loc.cpu().numpy().tolist() == ref.kv_locations.tolist()
+    for st, sl in zip(ostates, seq_lens):
+        st.seq_len += sl
+
+
+def test_pack_multi_step_with_reuse(gpu):
+    ps = 16
+    cfg, kv, mgr = _setup(gpu, max_pages=3000, ps=ps)
+    bufs = WorkspaceBufferManager(64 << 20, gpu)
+    opool = P.FifoPages(3000)
+    rng = np.random.default_rng(0)
+    rids = [f"r{i}" for i in range(40)]
+    for r in rids:
+        mgr.add_request(r, ["main"])
+    ostate = {r: P.ReqState() for r in rids}
+    live = list(rids)
+    for step in range(12):
+        if step == 0:
+            seq_lens = rng.integers(1, 900, size=len(live)).tolist()  # prefill
+        elif step % 4 == 3:
+            seq_lens = rng.integers(0, 40, size=len(live)).tolist()   # ragged chunk, zeros allowed
+        else:
+            seq_lens = [1] * len(live)                                  # decode
+        cm = BatchedCacheManager(live, {r: "main" for r in live}, kv, mgr, bufs, cfg, gpu)
+        log(f"pack step {step}: B={len(live)} tokens={sum(seq_lens)}")
+        _check_step(cm, live, "main", seq_lens, [ostate[r] for r in live], opool, ps)
+        for r, sl in zip(live, seq_lens):
+            mgr.get_state(r, "main").seq_len += sl
+        if step % 3 == 2:  # finish a few requests, start new ones: pages get reused
+            for r in list(live[:5]):
+                mgr.remove_request(r)
+                opool.give(ostate[r].pages)
+                live.remove(r)
+            for j in range(5):
+                r = f"n{step}_{j}"
+                mgr.add_request(r, ["main"])
+                ostate[r] = P.ReqState()
+                live.append(r)
+
+
+def test_pack_allocation_failure_is_raised_before_launch(gpu):
+    cfg, kv, mgr = _setup(gpu, max_pages=10)
+    bufs = WorkspaceBufferManager(16 << 20, gpu)
+    for r in ("a", "b"):
+        mgr.add_request(r, ["main"])
+    cm = BatchedCacheManager(["a", "b"], {"a": "main", "b": "main"}, kv, mgr, bufs, cfg, gpu)
+    with pytest.raises(AllocationFailedError) as e:
+        cm.plan_attention([100, 100])
+    assert e.value.request_id == "b" and e.value.pages_short == 4  # 7 pages asked, 3 left
+    assert len(mgr.get_state("a", "main").page_indices) == 7  # earlier request keeps its pages
+
+
+def _split_layout(batch, nkv, d, units=8192):
+    target = max(16, units // nkv)
+    max_chunks = target + batch  # the workspace below is large enough for the full budget
+    align = lambda x: (x + 255) // 256 * 256
+    hdr = 0
+    chunk_indptr = 256
+    work = align(chunk_indptr + 4 * (batch + 1))
+    return hdr, chunk_indptr, work, max_chunks
+
+
+def test_decode_plan_partition(gpu):
+    from gpu_helpers import custom_batch
+
+    lens = [0, 1, 16, 17, 300, 5000, 32768, 4096, 77]
+    qo, kv_indptr, kv_indices, last = custom_batch(lens, 16, 4000, seed=2)
+    hq, hkv, d = 32, 4, 128
+    ws = workspace(gpu, 256 << 20)
+    loc = torch.full((len(lens), 2), -7, dtype=torch.long, device=gpu)
+    ti = lambda x: torch.as_tensor(x).to(gpu)
+    a, b_, c = ti(kv_indptr), ti(kv_indices), ti(last)
+    _lib.check(_lib.lib().mi_decode_plan(None, a.data_ptr(), b_.data_ptr(), c.data_ptr(), len(lens), 16, hq, hkv, d,
+                                         loc.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_ptr()), "plan")
+    torch.cuda.synchronize()
+    hdr, ci, wk, max_chunks = _split_layout(len(lens), hkv, d)
+    h = ws[hdr:hdr + 20].cpu().view(torch.int32).tolist()
+    cp, nchunks = P.split_chunks(kv_indptr, 16, 8192, hkv)
+    assert h[0] == 0x4D494450 and h[1] == len(lens) and h[3] == cp and h[2] == int(nchunks.sum())
+    cptr = ws[ci:ci + 4 * (len(lens) + 1)].cpu().view(torch.int32).numpy()
+    assert cptr.tolist() == [0] + np.cumsum(nchunks).tolist()
+    work = ws[wk:wk + 16 * h[2]].cpu().view(torch.int32).numpy().reshape(-1, 4)
+    npages = np.diff(kv_indptr)
+    for r in range(len(lens)):
+        rows = work[cptr[r]:cptr[r + 1]]
+        assert (rows[:, 0] == r).all() and (rows[:, 3] == nchunks[r]).all()
+        covered = [p for lo, hi in rows[:, 1:3] for p in range(lo, hi)]
+        assert covered == list(range(npages[r]))
+    # locations: (last page, last_page_len - 1); (-1, -1) for a request without pages
+    exp = []
+    for r in range(len(lens)):
+        if npages[r] == 0:
+            exp.append([-1, -1])
+        else:
+            exp.append([int(kv_indices[kv_indptr[r + 1] - 1]), int(last[r]) - 1])
+    assert loc.cpu().tolist() == exp
