@@ -179,6 +179,24 @@ def cpu_baseline(bt, kv_gpu, q, k, v, budget_s: float = 12.0):
     }
 
 
+def copy_calibration(dev) -> int:
+    """A plain copy of 1 GiB, three times: 1 GiB read + 1 GiB written per launch."""
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev[0].record()
+    for i in range(3):
+        dst.copy_(src)
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(3)]
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "ms": ms,
+                      "copy_GBps_read_plus_write": [2 * n / (m * 1e-3) / 1e9 for m in ms]}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -186,6 +204,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of 1 GiB (3x): the reference point that scales "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -193,6 +214,8 @@ def main() -> int:
         return 2
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        return copy_calibration(dev)
     _lib.lib()
     _log(f"setup {args.config} ...")
     bt, cfg, kv, mgr, cm, rids, q, k, v = setup(args.config, dev)

@@ -127,6 +127,40 @@ MI_DEVICE int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 MI_DEVICE float xor_shuffle(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 
+// max / sum over the four lanes {l, l^16, l^32, l^48} (the four 16-lane rows
+// holding one MFMA column), on the VALU: v_permlane32_swap pairs lane l with
+// l^32 and v_permlane16_swap pairs row r with row r^1; taking both outputs of
+// each swap makes the result independent of which operand receives which half.
+MI_DEVICE float rows4_max(float x) {
+  const uint32_t u = bitcast<uint32_t>(x);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const float y = fmaxf(bitcast<float>((uint32_t)a[0]), bitcast<float>((uint32_t)a[1]));
+  const uint32_t v = bitcast<uint32_t>(y);
+  const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return fmaxf(bitcast<float>((uint32_t)b[0]), bitcast<float>((uint32_t)b[1]));
+}
+MI_DEVICE float rows4_sum(float x) {
+  const uint32_t u = bitcast<uint32_t>(x);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const float y = bitcast<float>((uint32_t)a[0]) + bitcast<float>((uint32_t)a[1]);
+  const uint32_t v = bitcast<uint32_t>(y);
+  const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return bitcast<float>((uint32_t)b[0]) + bitcast<float>((uint32_t)b[1]);
+}
+
+// Streaming (non-temporal) global loads: KV pages are read once per launch.
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+MI_DEVICE uint4 nt_load16(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+MI_DEVICE uint2 nt_load8(const void* p) {
+  const u32x2_t v = __builtin_nontemporal_load((const u32x2_t*)p);
+  return make_uint2(v.x, v.y);
+}
+MI_DEVICE uint32_t nt_load4(const void* p) { return __builtin_nontemporal_load((const uint32_t*)p); }
+
 // v_perm_b32: byte i of the result = byte sel[i] of {hi:lo} where selector
 // values 0-3 address `lo` and 4-7 address `hi`.
 MI_DEVICE uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {

@@ -16,9 +16,13 @@
 //             S^T[16 tok x 16 rows] = K[16 x D] . Q^T      (v_mfma 16x16x32)
 //             online softmax on S (fp32, exp2 domain)
 //             O^T[D x 16 rows]     += V^T[D x 16 tok] . P^T (v_mfma 16x16x16)
-//           K rows are read as 64-byte row segments, V rows as whole
-//           head_dim rows (D*2 bytes) per 16 lanes: every 128-bit load is
-//           fully used.  V is transposed in registers (v_perm_b32): output
+//           K and V rows are read as whole head_dim rows (16 lanes x 128 bits
+//           per row for D=128) with non-temporal loads, two tiles ahead of the
+//           MFMA work.  The MFMA A operand wants one token per lane%16, which
+//           a register-only layout can only feed with 64-byte row segments
+//           (measured ~15% slower to stream from HBM), so K passes through a
+//           small per-wave LDS buffer: ds_write of the rows, ds_read of the
+//           fragments.  V is transposed in registers (v_perm_b32): output
 //           column d is permuted as d = (D/16)*m + tile, which turns the
 //           transpose into a 4x(D/16) shuffle inside each lane.
 //   merge : log-sum-exp merge of the chunk partials of split requests.
@@ -163,29 +167,29 @@ template <bool FP8, int D>
 struct TileRegs;
 
 template <int D>
-struct TileRegs<false, D> {  // 16-bit KV: K as MFMA A fragments, V as row slices
-  uint4 k[D / 32];
-  uint32_t v[4][D / 32];  // D/16 elements (16-bit) per row
+struct TileRegs<false, D> {  // 16-bit KV: K and V as row slices (D/16 elements per row)
+  uint32_t k[4][D / 32];
+  uint32_t v[4][D / 32];
 };
 
 template <int D>
-struct TileRegs<true, D> {  // fp8 KV: raw bytes, converted right before use
-  uint2 k[D / 32];
-  uint32_t v[4][D / 64 > 0 ? D / 64 : 1];  // D/16 bytes per row
+struct TileRegs<true, D> {  // fp8 KV: raw bytes (D/16 per row), converted right before use
+  uint32_t k[4][D / 64 > 0 ? D / 64 : 1];
+  uint32_t v[4][D / 64 > 0 ? D / 64 : 1];
 };
 
 template <int N>
 MI_DEVICE void load_words(uint32_t (&dst)[N], const uint8_t* src) {
   if constexpr (N == 1) {
-    dst[0] = *(const uint32_t*)src;
+    dst[0] = nt_load4(src);
   } else if constexpr (N == 2) {
-    const uint2 t = *(const uint2*)src;
+    const uint2 t = nt_load8(src);
     dst[0] = t.x;
     dst[1] = t.y;
   } else {
 #pragma unroll
     for (int i = 0; i < N; i += 4) {
-      const uint4 t = *(const uint4*)(src + 4 * i);
+      const uint4 t = nt_load16(src + 4 * i);
       dst[i] = t.x;
       dst[i + 1] = t.y;
       dst[i + 2] = t.z;
@@ -199,7 +203,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   constexpr int KS = D / 32;  // MFMA k-steps over head_dim for S
   constexpr int VW = D / 16;  // V elements per lane per row == output d-tiles
   constexpr int ESZ = FP8 ? 1 : 2;
+  constexpr int KRS = D * 2 + 16;  // LDS row stride of the K transpose buffer (padded)
   constexpr float kNegInf = -__builtin_inff();
+  // Per-wave K staging: rows arrive as whole head_dim rows and leave as MFMA
+  // A fragments (row = token, 8 consecutive d per lane).
+  __shared__ __attribute__((aligned(16))) uint8_t lds_k[4][16 * KRS];
 
   const int lane = lane_id();
   const int wave = uniform((int)threadIdx.x >> 6);
@@ -255,8 +263,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 
   const uint8_t* kv = (const uint8_t*)p.kv;
   const int64_t head_off = (int64_t)h * p.head_stride * ESZ;
-  // per-lane byte offsets inside a tile (relative to the tile's first K row)
-  const uint32_t koff = (uint32_t)(col * p.token_stride + 8 * grp) * ESZ;
+  // per-lane byte offset inside a tile: rows 4*grp + r, elements [VW*col, VW*col + VW)
   const uint32_t voff0 = (uint32_t)((4 * grp) * p.token_stride + VW * col) * ESZ;
   const uint32_t vrow = (uint32_t)(p.token_stride * ESZ);
   const int64_t kvhalf = p.kv_stride * ESZ;
@@ -265,35 +272,14 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     return kv + (int64_t)page * p.page_stride * ESZ + (int64_t)r0 * p.token_stride * ESZ + head_off;
   };
   auto load_tile = [&](TileRegs<FP8, D>& t, const uint8_t* base) {
+    const uint8_t* kb = base + voff0;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      if constexpr (FP8)
-        t.k[s] = *(const uint2*)(base + koff + 32 * s);
-      else
-        t.k[s] = *(const uint4*)(base + koff + 64 * s);
-    }
-    const uint8_t* vb = base + kvhalf + voff0;
+    for (int r = 0; r < 4; ++r) load_words(t.k[r], kb + r * vrow);
+    const uint8_t* vb = kb + kvhalf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) load_words(t.v[r], vb + r * vrow);
   };
-  // Page ids of the chunk, 64 at a time in a VGPR (lane i: page pg0+win+i);
-  // v_readlane hands the tile's page to the scalar unit without a memory
-  // round trip inside the pipelined loop.
-  int win = 0;
-  auto load_window = [&](int w0) -> int {
-    const int idx = pg0 + w0 + lane;
-    return idx < pg1 ? p.kv_indices[page_base + idx] : 0;
-  };
-  int pwin = load_window(0);
-  auto page_of_tile = [&](int t) -> int {
-    const int local = (16 * t) / ps;  // tok_begin is page aligned
-    if (local - win >= 64) {
-      win += 64;
-      pwin = load_window(win);
-    }
-    return __builtin_amdgcn_readlane(pwin, local - win);
-  };
-  auto row0_of_tile = [&](int t) -> int { return (16 * t) % ps; };
+  uint8_t* kst = &lds_k[wave][0];
 
   f32x4 acc[VW];
 #pragma unroll
@@ -302,19 +288,33 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 
   auto compute_tile = [&](TileRegs<FP8, D>& t, int ti) {
     const int tb = tok_begin + 16 * ti;
-    // ---- S^T = K . Q^T
+    // ---- K rows -> LDS (row 4*grp + r, elements [VW*col, +VW)) -> A fragments
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      uint32_t w[VW / 2];
+      if constexpr (FP8) {
+#pragma unroll
+        for (int i = 0; i < VW / 4; ++i) {
+          w[2 * i] = fp8x2_to_mt<MT>(t.k[r][i], false);
+          w[2 * i + 1] = fp8x2_to_mt<MT>(t.k[r][i], true);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < VW / 2; ++i) w[i] = t.k[r][i];
+      }
+      uint8_t* dst = kst + (4 * grp + r) * KRS + VW * 2 * col;
+      if constexpr (VW == 4) {
+        *(uint2*)dst = make_uint2(w[0], w[1]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 4 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+      }
+    }
+    // ---- S^T = K . Q^T  (A fragment: row col, elements 8*grp + 32*st .. +8)
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < KS; ++st) {
-      uint4 a;
-      if constexpr (FP8) {
-        a.x = fp8x2_to_mt<MT>(t.k[st].x, false);
-        a.y = fp8x2_to_mt<MT>(t.k[st].x, true);
-        a.z = fp8x2_to_mt<MT>(t.k[st].y, false);
-        a.w = fp8x2_to_mt<MT>(t.k[st].y, true);
-      } else {
-        a = t.k[st];
-      }
+      const uint4 a = *(const uint4*)(kst + col * KRS + (8 * grp + 32 * st) * 2);
       s = MT::mma_16x16x32(a, qf[st], s);
     }
     float sv[4];
@@ -333,9 +333,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
       }
     }
     // ---- online softmax (row = col; the 4 lane groups share a row)
-    float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mt = fmaxf(mt, xor_shuffle(mt, 16));
-    mt = fmaxf(mt, xor_shuffle(mt, 32));
+    const float mt = rows4_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
     const float m_new = fmaxf(m_run, mt);
     const float m_use = m_new == kNegInf ? 0.f : m_new;
     const float alpha = fast_exp2(m_run - m_use);
@@ -378,29 +376,44 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     }
   };
 
-  // ---- software-pipelined tile loop: loads of tile t+1 overlap compute of t
-  if (ntiles > 0) {
-    TileRegs<FP8, D> A, B;
-    int pg_next = page_of_tile(0);
-    load_tile(A, tile_base(pg_next, row0_of_tile(0)));
-    if (ntiles > 1) pg_next = page_of_tile(1);
+  // ---- tile loop, in windows of 64 pages.  The window's page ids sit in one
+  // VGPR (lane i: page i of the window) and v_readlane hands each tile's page
+  // to the scalar unit, so no memory access sits between the loads of
+  // consecutive tiles; inside a window the loads run two tiles ahead of the
+  // MFMA work (three register buffers).
+  const int tiles_per_win = 4 * ps;  // 64 pages of ps/16 tiles
+  for (int w0 = 0; w0 < ntiles; w0 += tiles_per_win) {
+    const int wt = min(tiles_per_win, ntiles - w0);
+    const int first = pg0 + (16 * w0) / ps;
+    const int pwin = first + lane < pg1 ? p.kv_indices[page_base + first + lane] : 0;
+    auto tile_ptr = [&](int t) -> const uint8_t* {  // t: tile within the window
+      return tile_base(__builtin_amdgcn_readlane(pwin, (16 * t) / ps), (16 * (w0 + t)) % ps);
+    };
+    TileRegs<FP8, D> A, B, C;
+    load_tile(A, tile_ptr(0));
+    if (wt > 1) load_tile(B, tile_ptr(1));
     int t = 0;
-    for (; t + 1 < ntiles; t += 2) {
-      load_tile(B, tile_base(pg_next, row0_of_tile(t + 1)));
-      if (t + 2 < ntiles) pg_next = page_of_tile(t + 2);
-      compute_tile(A, t);
-      if (t + 2 < ntiles) {
-        load_tile(A, tile_base(pg_next, row0_of_tile(t + 2)));
-        if (t + 3 < ntiles) pg_next = page_of_tile(t + 3);
-      }
-      compute_tile(B, t + 1);
+    // Steady state: every load in the body is in range, so the compiler's
+    // vmcnt waits stay exact (two tiles in flight while one is computed).
+    for (; t + 4 < wt; t += 3) {
+      load_tile(C, tile_ptr(t + 2));
+      compute_tile(A, w0 + t);
+      load_tile(A, tile_ptr(t + 3));
+      compute_tile(B, w0 + t + 1);
+      load_tile(B, tile_ptr(t + 4));
+      compute_tile(C, w0 + t + 2);
     }
-    if (t < ntiles) compute_tile(A, t);
+    // Tail: at most four tiles left; A holds tile t, B tile t+1.
+    if (t + 2 < wt) load_tile(C, tile_ptr(t + 2));
+    if (t < wt) compute_tile(A, w0 + t);
+    if (t + 3 < wt) load_tile(A, tile_ptr(t + 3));
+    if (t + 1 < wt) compute_tile(B, w0 + t + 1);
+    if (t + 2 < wt) compute_tile(C, w0 + t + 2);
+    if (t + 3 < wt) compute_tile(A, w0 + t + 3);
   }
 
   // ---- epilogue
-  float l_tot = l_run + xor_shuffle(l_run, 16);
-  l_tot += xor_shuffle(l_tot, 32);
+  const float l_tot = rows4_sum(l_run);
   const float inv = l_tot > 0.f ? vscale / l_tot : 0.f;
   if (!row_valid) return;
   if (nchunks_b == 1) {
@@ -461,22 +474,51 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p) {
   float acc[VW];
 #pragma unroll
   for (int i = 0; i < VW; ++i) acc[i] = 0.f;
+  // partial (chunk c) of this row: lse at lse_part[pc(c)], o at o_part[pc(c) * D]
+  const int64_t pstride = (int64_t)nkv * kRows;
+  const int64_t p0 = ((int64_t)c0 * nkv + h) * kRows + n;
   float M = kNegInf;
-  for (int c = 0; c < nb; ++c) M = fmaxf(M, p.lse_part[((int64_t)(c0 + c) * nkv + h) * kRows + n]);
+#pragma unroll 8
+  for (int c = 0; c < nb; ++c) M = fmaxf(M, p.lse_part[p0 + c * pstride]);
   float wsum = 0.f;
   if (M != kNegInf) {
-    for (int c = 0; c < nb; ++c) {
-      const int64_t pi = ((int64_t)(c0 + c) * nkv + h) * kRows + n;
+    // four partials per step: their loads are independent and overlap
+    constexpr int U = 4;
+    int c = 0;
+    for (; c + U <= nb; c += U) {
+      float w[U];
+      float4 o[U][VW / 4];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t pi = p0 + (c + u) * pstride;
+        w[u] = p.lse_part[pi];
+#pragma unroll
+        for (int i = 0; i < VW / 4; ++i) o[u][i] = *(const float4*)(p.o_part + pi * D + VW * seg + 4 * i);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float wgt = fast_exp2(w[u] - M);
+        wsum += wgt;
+#pragma unroll
+        for (int i = 0; i < VW / 4; ++i) {
+          acc[4 * i] += wgt * o[u][i].x;
+          acc[4 * i + 1] += wgt * o[u][i].y;
+          acc[4 * i + 2] += wgt * o[u][i].z;
+          acc[4 * i + 3] += wgt * o[u][i].w;
+        }
+      }
+    }
+    for (; c < nb; ++c) {
+      const int64_t pi = p0 + c * pstride;
       const float wgt = fast_exp2(p.lse_part[pi] - M);
       wsum += wgt;
-      const float* src = p.o_part + pi * D + VW * seg;
 #pragma unroll
-      for (int i = 0; i < VW; i += 4) {
-        const float4 o = *(const float4*)(src + i);
-        acc[i] += wgt * o.x;
-        acc[i + 1] += wgt * o.y;
-        acc[i + 2] += wgt * o.z;
-        acc[i + 3] += wgt * o.w;
+      for (int i = 0; i < VW / 4; ++i) {
+        const float4 o = *(const float4*)(p.o_part + pi * D + VW * seg + 4 * i);
+        acc[4 * i] += wgt * o.x;
+        acc[4 * i + 1] += wgt * o.y;
+        acc[4 * i + 2] += wgt * o.z;
+        acc[4 * i + 3] += wgt * o.w;
       }
     }
   }

@@ -283,8 +283,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
           sv[js][r] = x;
           mt = fmaxf(mt, x);
         }
-      mt = fmaxf(mt, xor_shuffle(mt, 16));
-      mt = fmaxf(mt, xor_shuffle(mt, 32));
+      mt = rows4_max(mt);
       const float m_new = fmaxf(m_run[rg], mt);
       const float m_use = m_new == kNegInf ? 0.f : m_new;
       const float alpha = fast_exp2(m_run[rg] - m_use);
@@ -362,8 +361,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
   // ---- epilogue
 #pragma unroll
   for (int rg = 0; rg < 2; ++rg) {
-    float l_tot = l_run[rg] + xor_shuffle(l_run[rg], 16);
-    l_tot += xor_shuffle(l_tot, 32);
+    const float l_tot = rows4_sum(l_run[rg]);
     const float inv = l_tot > 0.f ? vscale / l_tot : 0.f;
     const int n = row0 + 32 * wave + 16 * rg + col;
     if (n >= rows_total) continue;
