@@ -7,12 +7,14 @@
 //
 // Work decomposition
 //   plan  : one 1024-thread workgroup splits every request's page list into
-//           chunks of `chunk_pages` pages (chunk_pages chosen on the GPU from
-//           the batch's total page count so the machine gets ~8K wave units)
-//           and writes the chunk list into the caller's workspace.
-//   decode: one wavefront per (chunk, kv-head).  Its 16 MFMA columns are the
-//           (query token, q-head-in-group) rows that share that kv-head, so
-//           K/V are loaded from HBM once per GQA group.  Per 16-token tile:
+//           items of at most `item_pages` pages (chosen on the GPU from the
+//           batch's total page count so the machine gets ~8K wavefronts) and
+//           writes the item list into the caller's workspace.
+//   decode: one workgroup per (item, kv-head); its 4 wavefronts take
+//           contiguous quarters of the item's 16-token tiles.  A wavefront's
+//           16 MFMA columns are the (query token, q-head-in-group) rows that
+//           share the kv-head, so K/V are read from HBM once per GQA group.
+//           Per tile:
 //             S^T[16 tok x 16 rows] = K[16 x D] . Q^T      (v_mfma 16x16x32)
 //             online softmax on S (fp32, exp2 domain)
 //             O^T[D x 16 rows]     += V^T[D x 16 tok] . P^T (v_mfma 16x16x16)
@@ -25,7 +27,14 @@
 //           fragments.  V is transposed in registers (v_perm_b32): output
 //           column d is permuted as d = (D/16)*m + tile, which turns the
 //           transpose into a 4x(D/16) shuffle inside each lane.
-//   merge : log-sum-exp merge of the chunk partials of split requests.
+//           The 4 wavefronts' softmax states are merged in LDS; an item that
+//           covers its whole request writes the final output, otherwise a
+//           partial (o, lse).  Partial stores are HBM writes interleaved with
+//           a read-saturated stream and cost far more than their bytes
+//           (measured: ~33 MB of partials added ~14% to the kernel), which
+//           is why an item spans 4 wavefronts' worth of pages.
+//   merge : log-sum-exp merge of the item partials of split requests, in the
+//           same register-order layout (whole-cache-line loads and stores).
 #include <stdlib.h>
 
 #include "mi_common.h"
@@ -34,12 +43,13 @@
 namespace mi {
 
 constexpr int kRows = 16;             // MFMA N: query rows per wave
-constexpr int kMinChunkTokens = 256;  // never split a request finer than this
+constexpr int kMinChunkTokens = 1024;  // never split a request finer than this (4 waves x 256)
 
 
-// Target number of KV chunks for one plan: ~8K (chunk, kv-head) wave units
-// keeps 256 CUs x 4 SIMDs busy with a short tail.  MSTAR_DECODE_TARGET_UNITS
-// overrides it for tuning sweeps (read once per process).
+// Target number of wavefronts for one plan: ~8K (item, kv-head, quarter)
+// wave units keeps 256 CUs x 4 SIMDs busy with a short tail.
+// MSTAR_DECODE_TARGET_UNITS overrides it for tuning sweeps (read once per
+// process).
 static int32_t decode_target_units() {
   static const int32_t units = [] {
     const char* e = getenv("MSTAR_DECODE_TARGET_UNITS");
@@ -51,7 +61,7 @@ static int32_t decode_target_units() {
 
 SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t ws_avail) {
   SplitLayout L;
-  int32_t target = decode_target_units() / (nkv > 0 ? nkv : 1);
+  int32_t target = decode_target_units() / (4 * (nkv > 0 ? nkv : 1));  // 4 waves per item
   if (target < 16) target = 16;
   int64_t max_chunks = (int64_t)target + batch;
   if (ws_avail >= 0) {  // fewer, longer chunks when the caller's workspace is smaller
@@ -92,31 +102,47 @@ struct PlanParams {
   int64_t* kv_locations;
 };
 
+// Work list order: longest first.  Every request's full items (item_pages
+// pages) come first, then the requests' shorter remainder items in
+// descending size (64 size buckets, counting sort in LDS): the last
+// workgroups to start are the shortest, so the machine drains evenly instead
+// of waiting on full-size items that started late.  An item is
+// (request, index within the request, end page, items of the request); its
+// partial lives at chunk_indptr[request] + index whatever its list position.
+constexpr int kSizeBuckets = 64;
+
 __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
   __shared__ int smem[16];
+  __shared__ int s_bucket[kSizeBuckets];
   const int total_pages = p.kv_indptr[p.batch] - p.kv_indptr[0];
   int cp = (total_pages + p.target - 1) / p.target;
   if (cp < p.min_chunk_pages) cp = p.min_chunk_pages;
-  int carry = 0;
+  if (threadIdx.x < kSizeBuckets) s_bucket[threadIdx.x] = 0;
+  __syncthreads();
+  auto items_of = [&](int b, int& np, int& n, int& full, int& rem_bucket) {
+    np = p.kv_indptr[b + 1] - p.kv_indptr[b];
+    n = np > 0 ? (np + cp - 1) / cp : 0;
+    if (p.qo_indptr) {  // ragged batch: only short-query requests belong to this kernel
+      const int qo_len = p.qo_indptr[b + 1] - p.qo_indptr[b];
+      if (qo_len <= 0 || qo_len * p.group > kRows) n = 0;
+    }
+    full = n > 0 ? np / cp : 0;
+    const int rem = n > 0 ? np - full * cp : 0;
+    rem_bucket = rem > 0 ? (int)(((int64_t)rem * kSizeBuckets - 1) / cp) : -1;
+  };
+  // pass 1: item offsets per request, full items in place, remainder histogram
+  int carry = 0, carry_full = 0;
   for (int base = 0; base < p.batch; base += 1024) {
     const int b = base + (int)threadIdx.x;
-    int np = 0, n = 0;
-    if (b < p.batch) {
-      np = p.kv_indptr[b + 1] - p.kv_indptr[b];
-      n = np > 0 ? (np + cp - 1) / cp : 0;
-      if (p.qo_indptr) {  // ragged batch: only short-query requests belong to this kernel
-        const int qo_len = p.qo_indptr[b + 1] - p.qo_indptr[b];
-        if (qo_len <= 0 || qo_len * p.group > kRows) n = 0;
-      }
-    }
-    int total;
+    int np = 0, n = 0, full = 0, rb = -1;
+    if (b < p.batch) items_of(b, np, n, full, rb);
+    int total, total_full;
     const int first = block_exclusive_scan_1024(n, total, smem) + carry;
+    const int ffirst = block_exclusive_scan_1024(full, total_full, smem) + carry_full;
     if (b < p.batch) {
       p.chunk_indptr[b] = first;
-      for (int c = 0; c < n && first + c < p.max_chunks; ++c) {
-        const int p0 = c * cp;
-        p.work[first + c] = make_int4(b, p0, min(p0 + cp, np), n);
-      }
+      for (int c = 0; c < full && ffirst + c < p.max_chunks; ++c) p.work[ffirst + c] = make_int4(b, c, (c + 1) * cp, n);
+      if (rb >= 0) atomicAdd(&s_bucket[rb], 1);
       if (p.kv_locations) {
         int64_t page = -1, pos = -1;
         if (np > 0) {
@@ -128,6 +154,30 @@ __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
       }
     }
     carry += total;
+    carry_full += total_full;
+  }
+  __syncthreads();
+  // bucket start positions, largest bucket first, after all full items
+  if (threadIdx.x == 0) {
+    int off = carry_full;
+    for (int k = kSizeBuckets - 1; k >= 0; --k) {
+      const int c = s_bucket[k];
+      s_bucket[k] = off;
+      off += c;
+    }
+  }
+  __syncthreads();
+  // pass 2: remainder items
+  for (int base = 0; base < p.batch; base += 1024) {
+    const int b = base + (int)threadIdx.x;
+    if (b < p.batch) {
+      int np, n, full, rb;
+      items_of(b, np, n, full, rb);
+      if (rb >= 0) {
+        const int pos = atomicAdd(&s_bucket[rb], 1);
+        if (pos < p.max_chunks) p.work[pos] = make_int4(b, full, np, n);
+      }
+    }
   }
   if (threadIdx.x == 0) {
     p.chunk_indptr[p.batch] = carry;
@@ -204,20 +254,26 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   constexpr int VW = D / 16;  // V elements per lane per row == output d-tiles
   constexpr int ESZ = FP8 ? 1 : 2;
   constexpr int KRS = D * 2 + 16;  // LDS row stride of the K transpose buffer (padded)
+  constexpr int NS = VW / 4;       // float4 groups per lane per output row segment
   constexpr float kNegInf = -__builtin_inff();
-  // Per-wave K staging: rows arrive as whole head_dim rows and leave as MFMA
-  // A fragments (row = token, 8 consecutive d per lane).
-  __shared__ __attribute__((aligned(16))) uint8_t lds_k[4][16 * KRS];
+  // LDS: during the tile loop, per-wave K staging (rows arrive as whole
+  // head_dim rows and leave as MFMA A fragments); after it, the 4 waves'
+  // softmax states for the in-workgroup merge.
+  constexpr int kStageBytes = 4 * 16 * KRS;
+  constexpr int kMergeBytes = 4 * (4 * NS * 64 * 16);
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes];
+  __shared__ float lds_m[4][kRows], lds_l[4][kRows];
 
   const int lane = lane_id();
   const int wave = uniform((int)threadIdx.x >> 6);
   const int nkv = p.num_kv_heads;
-  const int unit = (int)blockIdx.x * 4 + wave;
-  const int chunk = uniform(unit / nkv);
-  const int h = unit - chunk * nkv;
-  if (chunk >= p.hdr[kHdrChunks]) return;
-  const int4 wk = p.work[chunk];
-  const int b = uniform(wk.x), pg0 = uniform(wk.y), pg1 = uniform(wk.z), nchunks_b = uniform(wk.w);
+  // workgroup = (item, kv-head); its 4 waves split the item's tiles
+  const int item = uniform((int)blockIdx.x / nkv);
+  const int h = (int)blockIdx.x - item * nkv;
+  if (item >= p.hdr[kHdrChunks]) return;  // uniform across the workgroup
+  const int4 wk = p.work[item];
+  const int b = uniform(wk.x), kidx = uniform(wk.y), pg1 = uniform(wk.z), nitems_b = uniform(wk.w);
+  const int pg0 = kidx * p.hdr[kHdrChunkPages];
 
   const int ps = p.page_size;
   const int page_base = p.kv_indptr[b];
@@ -230,9 +286,14 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   }
   const int G = p.group;
   const int rows = min(qo_len * G, kRows);
-  const int tok_begin = pg0 * ps;
-  const int tok_end = min(pg1 * ps, kv_len);
-  const int ntiles = tok_end > tok_begin ? (tok_end - tok_begin + 15) >> 4 : 0;
+  const int item_tok0 = pg0 * ps;
+  const int item_tok1 = min(pg1 * ps, kv_len);
+  const int item_tiles = item_tok1 > item_tok0 ? (item_tok1 - item_tok0 + 15) >> 4 : 0;
+  // this wave's contiguous quarter of the item's tiles
+  const int tq = item_tiles >> 2, trem = item_tiles & 3;
+  const int my_t0 = wave * tq + min(wave, trem);
+  const int ntiles = tq + (wave < trem ? 1 : 0);
+  const int tok_begin = item_tok0 + 16 * my_t0;
 
   const int col = lane & 15;  // query row handled in MFMA column `col`
   const int grp = lane >> 4;  // 0..3
@@ -279,7 +340,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) load_words(t.v[r], vb + r * vrow);
   };
-  uint8_t* kst = &lds_k[wave][0];
+  uint8_t* kst = &lds[wave * 16 * KRS];
 
   f32x4 acc[VW];
 #pragma unroll
@@ -381,13 +442,14 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   // to the scalar unit, so no memory access sits between the loads of
   // consecutive tiles; inside a window the loads run two tiles ahead of the
   // MFMA work (three register buffers).
-  const int tiles_per_win = 4 * ps;  // 64 pages of ps/16 tiles
-  for (int w0 = 0; w0 < ntiles; w0 += tiles_per_win) {
-    const int wt = min(tiles_per_win, ntiles - w0);
-    const int first = pg0 + (16 * w0) / ps;
+  for (int w0 = 0; w0 < ntiles;) {
+    const int wtok = tok_begin + 16 * w0;  // first token of the window
+    const int first = wtok / ps;           // its page (request-relative)
+    const int wt = min(ntiles - w0, ((first + 64) * ps - wtok) >> 4);
     const int pwin = first + lane < pg1 ? p.kv_indices[page_base + first + lane] : 0;
     auto tile_ptr = [&](int t) -> const uint8_t* {  // t: tile within the window
-      return tile_base(__builtin_amdgcn_readlane(pwin, (16 * t) / ps), (16 * (w0 + t)) % ps);
+      const int tok = wtok + 16 * t;
+      return tile_base(__builtin_amdgcn_readlane(pwin, tok / ps - first), tok % ps);
     };
     TileRegs<FP8, D> A, B, C;
     load_tile(A, tile_ptr(0));
@@ -410,52 +472,98 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     if (t + 1 < wt) compute_tile(B, w0 + t + 1);
     if (t + 2 < wt) compute_tile(C, w0 + t + 2);
     if (t + 3 < wt) compute_tile(A, w0 + t + 3);
+    w0 += wt;
   }
 
-  // ---- epilogue
-  const float l_tot = rows4_sum(l_run);
-  const float inv = l_tot > 0.f ? vscale / l_tot : 0.f;
-  if (!row_valid) return;
-  if (nchunks_b == 1) {
-    uint16_t* orow = (uint16_t*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
-                     (int64_t)(h * G + g) * p.out_stride_head;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      uint32_t w[VW / 2];
-#pragma unroll
-      for (int i = 0; i < VW / 2; ++i) w[i] = MT::pack2(acc[2 * i][r] * inv, acc[2 * i + 1][r] * inv);
-      uint16_t* dst = orow + VW * (4 * grp + r);
-      if constexpr (VW == 4) {
-        *(uint2*)dst = make_uint2(w[0], w[1]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
-      }
+  // ---- epilogue: merge the 4 waves' states (m, l, acc) in LDS.  The acc
+  // register layout is the same in every wave (lane -> row col, elements
+  // d = VW*(4*grp + r) + j), so the merge is lane-local; wave w finishes the
+  // elements with r == w.
+  __syncthreads();  // all waves are done with their K staging buffers
+  {
+    const float l_row = rows4_sum(l_run);
+    if (grp == 0) {
+      lds_m[wave][col] = m_run;
+      lds_l[wave][col] = l_row;
     }
-  } else {
-    const int64_t pi = ((int64_t)chunk * nkv + h) * kRows + col;
-    float* orow = p.o_part + pi * D;
+    float4* st = (float4*)lds + (size_t)wave * 4 * NS * 64 + lane;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float* dst = orow + VW * (4 * grp + r);
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
       for (int j = 0; j < VW; j += 4)
-        *(float4*)(dst + j) = make_float4(acc[j][r] * inv, acc[j + 1][r] * inv, acc[j + 2][r] * inv,
-                                          acc[j + 3][r] * inv);
+        st[(r * NS + j / 4) * 64] = make_float4(acc[j][r], acc[j + 1][r], acc[j + 2][r], acc[j + 3][r]);
+  }
+  __syncthreads();
+  float M = kNegInf;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) M = fmaxf(M, lds_m[w][col]);
+  const float M_use = M == kNegInf ? 0.f : M;
+  float sc[4], L = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    sc[w] = fast_exp2(lds_m[w][col] - M_use);  // m = -inf -> 0
+    L += sc[w] * lds_l[w][col];
+  }
+  float4 o[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) o[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float4* src = (const float4*)lds + (size_t)w * 4 * NS * 64 + (size_t)wave * NS * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const float4 v = src[i * 64];
+      o[i].x += sc[w] * v.x;
+      o[i].y += sc[w] * v.y;
+      o[i].z += sc[w] * v.z;
+      o[i].w += sc[w] * v.w;
     }
-    if (grp == 0) p.lse_part[pi] = l_tot > 0.f ? m_run + fast_log2(l_tot) : kNegInf;
+  }
+  const float inv = L > 0.f ? vscale / L : 0.f;
+  if (!row_valid) return;
+  if (nitems_b == 1) {
+    // elements d = VW*(4*grp + wave) + [0, VW) of row col
+    uint16_t* dst = (uint16_t*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
+                    (int64_t)(h * G + g) * p.out_stride_head + VW * (4 * grp + wave);
+    uint32_t w[VW / 2];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      w[2 * i] = MT::pack2(o[i].x * inv, o[i].y * inv);
+      w[2 * i + 1] = MT::pack2(o[i].z * inv, o[i].w * inv);
+    }
+    if constexpr (VW == 4) {
+      *(uint2*)dst = make_uint2(w[0], w[1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+    }
+  } else {
+    // Partial (o, lse) of this item, o in register order: store index
+    // i = r*NS + j/4 of every lane is one contiguous 64 x 16-byte block.
+    const int64_t unit_idx = (int64_t)(p.chunk_indptr[b] + kidx) * nkv + h;
+    float* ob = p.o_part + unit_idx * kRows * D + 4 * lane;
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+      *(float4*)(ob + 256 * (wave * NS + i)) = make_float4(o[i].x * inv, o[i].y * inv, o[i].z * inv, o[i].w * inv);
+    if (wave == 0 && grp == 0) p.lse_part[unit_idx * kRows + col] = L > 0.f ? M + fast_log2(L) : kNegInf;
   }
 }
 
 // ----------------------------------------------------------------- merge
-// One workgroup per (request, kv-head): 16 rows x D, 16 threads per row.
+// One wavefront per (request, kv-head); lane l merges what lane l of the
+// decode wavefronts held: row l%16, output elements
+// d = VW*(4*(l/16) + r) + j, read from the register-order partial layout with
+// 64-lane contiguous (cache-line) loads.  Four wavefronts per workgroup.
 template <typename MT, int D>
-__global__ __launch_bounds__(256) void merge_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batch) {
   constexpr int VW = D / 16;
+  constexpr int NS = 4 * VW / 4;  // float4 stores per lane per partial
   constexpr float kNegInf = -__builtin_inff();
   const int nkv = p.num_kv_heads;
-  const int b = (int)blockIdx.x / nkv;
-  const int h = (int)blockIdx.x - b * nkv;
+  const int pair = (int)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
+  if (pair >= batch * nkv) return;
+  const int b = pair / nkv;
+  const int h = pair - b * nkv;
   const int c0 = p.chunk_indptr[b];
   const int nb = p.chunk_indptr[b + 1] - c0;
   if (nb == 1) return;  // written directly by the decode kernel
@@ -467,72 +575,80 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p) {
   const int G = p.group;
   if (qo_len * G > kRows) return;  // long-query request: written by the prefill kernel
   const int rows = qo_len * G;
-  const int n = (int)threadIdx.x >> 4;
-  const int seg = (int)threadIdx.x & 15;
-  if (n >= rows) return;
-  const int qtok = n / G, g = n - qtok * G;
-  float acc[VW];
+  const int lane = lane_id();
+  const int col = lane & 15, grp = lane >> 4;
+  if (col >= rows) return;
+  const int qtok = col / G, g = col - qtok * G;
+  float4 acc[NS];
 #pragma unroll
-  for (int i = 0; i < VW; ++i) acc[i] = 0.f;
-  // partial (chunk c) of this row: lse at lse_part[pc(c)], o at o_part[pc(c) * D]
-  const int64_t pstride = (int64_t)nkv * kRows;
-  const int64_t p0 = ((int64_t)c0 * nkv + h) * kRows + n;
+  for (int i = 0; i < NS; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int64_t u0 = (int64_t)c0 * nkv + h;  // unit of chunk c: u0 + c * nkv
   float M = kNegInf;
 #pragma unroll 8
-  for (int c = 0; c < nb; ++c) M = fmaxf(M, p.lse_part[p0 + c * pstride]);
+  for (int c = 0; c < nb; ++c) M = fmaxf(M, p.lse_part[(u0 + (int64_t)c * nkv) * kRows + col]);
   float wsum = 0.f;
   if (M != kNegInf) {
-    // four partials per step: their loads are independent and overlap
-    constexpr int U = 4;
+    constexpr int U = 2;  // partials in flight per step
     int c = 0;
     for (; c + U <= nb; c += U) {
       float w[U];
-      float4 o[U][VW / 4];
+      float4 o[U][NS];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t pi = p0 + (c + u) * pstride;
-        w[u] = p.lse_part[pi];
+        const int64_t unit = u0 + (int64_t)(c + u) * nkv;
+        w[u] = p.lse_part[unit * kRows + col];
+        const float* src = p.o_part + unit * kRows * D + 4 * lane;
 #pragma unroll
-        for (int i = 0; i < VW / 4; ++i) o[u][i] = *(const float4*)(p.o_part + pi * D + VW * seg + 4 * i);
+        for (int i = 0; i < NS; ++i) o[u][i] = *(const float4*)(src + 256 * i);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const float wgt = fast_exp2(w[u] - M);
         wsum += wgt;
 #pragma unroll
-        for (int i = 0; i < VW / 4; ++i) {
-          acc[4 * i] += wgt * o[u][i].x;
-          acc[4 * i + 1] += wgt * o[u][i].y;
-          acc[4 * i + 2] += wgt * o[u][i].z;
-          acc[4 * i + 3] += wgt * o[u][i].w;
+        for (int i = 0; i < NS; ++i) {
+          acc[i].x += wgt * o[u][i].x;
+          acc[i].y += wgt * o[u][i].y;
+          acc[i].z += wgt * o[u][i].z;
+          acc[i].w += wgt * o[u][i].w;
         }
       }
     }
     for (; c < nb; ++c) {
-      const int64_t pi = p0 + c * pstride;
-      const float wgt = fast_exp2(p.lse_part[pi] - M);
+      const int64_t unit = u0 + (int64_t)c * nkv;
+      const float wgt = fast_exp2(p.lse_part[unit * kRows + col] - M);
       wsum += wgt;
+      const float* src = p.o_part + unit * kRows * D + 4 * lane;
 #pragma unroll
-      for (int i = 0; i < VW / 4; ++i) {
-        const float4 o = *(const float4*)(p.o_part + pi * D + VW * seg + 4 * i);
-        acc[4 * i] += wgt * o.x;
-        acc[4 * i + 1] += wgt * o.y;
-        acc[4 * i + 2] += wgt * o.z;
-        acc[4 * i + 3] += wgt * o.w;
+      for (int i = 0; i < NS; ++i) {
+        const float4 o = *(const float4*)(src + 256 * i);
+        acc[i].x += wgt * o.x;
+        acc[i].y += wgt * o.y;
+        acc[i].z += wgt * o.z;
+        acc[i].w += wgt * o.w;
       }
     }
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  uint16_t* dst = (uint16_t*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
-                  (int64_t)(h * G + g) * p.out_stride_head + VW * seg;
-  uint32_t w[VW / 2];
+  uint16_t* orow = (uint16_t*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
+                   (int64_t)(h * G + g) * p.out_stride_head;
+  // store i = r*(VW/4) + j/4 holds d = VW*(4*grp + r) + j .. +3
 #pragma unroll
-  for (int i = 0; i < VW / 2; ++i) w[i] = MT::pack2(acc[2 * i] * inv, acc[2 * i + 1] * inv);
-  if constexpr (VW == 4) {
-    *(uint2*)dst = make_uint2(w[0], w[1]);
-  } else {
+  for (int r = 0; r < 4; ++r) {
+    uint32_t w[VW / 2];
 #pragma unroll
-    for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+    for (int jj = 0; jj < VW / 4; ++jj) {
+      const float4 a = acc[r * (VW / 4) + jj];
+      w[2 * jj] = MT::pack2(a.x * inv, a.y * inv);
+      w[2 * jj + 1] = MT::pack2(a.z * inv, a.w * inv);
+    }
+    uint16_t* dst = orow + VW * (4 * grp + r);
+    if constexpr (VW == 4) {
+      *(uint2*)dst = make_uint2(w[0], w[1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+    }
   }
 }
 
@@ -578,7 +694,8 @@ static void launch_decode(const DecodeParams& dp, int grid, int batch, int phase
   if (phases & kPhaseAttend)
     hipLaunchKernelGGL((decode_kernel<MT, FP8, D>), dim3(grid), dim3(256), 0, stream, dp);
   if ((phases & kPhaseMerge) && batch > 0)
-    hipLaunchKernelGGL((merge_kernel<MT, D>), dim3(batch * dp.num_kv_heads), dim3(256), 0, stream, dp);
+    hipLaunchKernelGGL((merge_kernel<MT, D>), dim3((batch * dp.num_kv_heads + 3) / 4), dim3(256), 0, stream, dp,
+                       batch);
 }
 
 template <typename MT, bool FP8>
@@ -642,7 +759,7 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
   dp.page_size = kv->page_size;
   dp.causal = causal ? 1 : 0;
   dp.scale_log2 = sm_scale * 1.4426950408889634f;
-  const int grid = (int)((L.max_chunks * (int64_t)nkv + 3) / 4);
+  const int grid = (int)(L.max_chunks * (int64_t)nkv);
   int st;
   if (q_dtype == MI_BF16)
     st = fp8 ? dispatch_d<BF16, true>(dp, D, grid, batch, phases, stream)

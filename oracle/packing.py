@@ -137,18 +137,18 @@ def decode_locations(kv_indptr, kv_indices, last_page_len) -> np.ndarray:
 
 
 def split_chunks(kv_indptr, page_size: int, target_units: int, num_kv_heads: int,
-                 min_chunk_tokens: int = 256) -> tuple[int, np.ndarray]:
-    """Split-KV partition rule of the GPU plan: (chunk_pages, chunks per request).
+                 min_chunk_tokens: int = 1024) -> tuple[int, np.ndarray]:
+    """Split-KV partition rule of the GPU plan: (item_pages, items per request).
 
-    chunk_pages = max(ceil(min_chunk_tokens/page_size), ceil(total_pages/target)),
-    target = max(16, target_units // num_kv_heads); each request's page list is
-    cut into ceil(pages/chunk_pages) consecutive chunks.  This is the build's
-    own schedule (FlashInfer's is not reproduced); the result must not depend
-    on it beyond rounding.
+    item_pages = max(ceil(min_chunk_tokens/page_size), ceil(total_pages/target)),
+    target = max(16, target_units // (4 * num_kv_heads)) (4 wavefronts per
+    item); each request's page list is cut into ceil(pages/item_pages)
+    consecutive items.  This is the build's own schedule (FlashInfer's is not
+    reproduced); the attention result must not depend on it beyond rounding.
     """
     kv_indptr = np.asarray(kv_indptr, dtype=np.int64)
     npages = np.diff(kv_indptr)
-    target = max(16, target_units // num_kv_heads)
+    target = max(16, target_units // (4 * num_kv_heads))
     total = int(kv_indptr[-1] - kv_indptr[0])
     cp = max(-(-min_chunk_tokens // page_size), -(-total // target))
     return cp, np.where(npages > 0, -(-npages // cp), 0)

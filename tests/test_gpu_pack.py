@@ -88,7 +88,7 @@ def test_pack_allocation_failure_is_raised_before_launch(gpu):
 
 
 def _split_layout(batch, nkv, d, units=8192):
-    target = max(16, units // nkv)
+    target = max(16, units // (4 * nkv))
     max_chunks = target + batch  # the workspace below is large enough for the full budget
     align = lambda x: (x + 255) // 256 * 256
     hdr = 0
@@ -118,10 +118,17 @@ def test_decode_plan_partition(gpu):
     assert cptr.tolist() == [0] + np.cumsum(nchunks).tolist()
     work = ws[wk:wk + 16 * h[2]].cpu().view(torch.int32).numpy().reshape(-1, 4)
     npages = np.diff(kv_indptr)
+    # items: (request, index within request, end page, items of request); start page = index * cp
+    sizes = [min(e, npages[r]) - k * cp for r, k, e, _ in work]
+    nfull = sum(1 for z in sizes if z == cp)
+    assert all(z == cp for z in sizes[:nfull]), f"full items come first: cp={cp} work={work.tolist()}"
+    buckets = [(z * 64 - 1) // cp for z in sizes[nfull:]]
+    assert buckets == sorted(buckets, reverse=True), "remainders ordered by descending size bucket"
     for r in range(len(lens)):
-        rows = work[cptr[r]:cptr[r + 1]]
-        assert (rows[:, 0] == r).all() and (rows[:, 3] == nchunks[r]).all()
-        covered = [p for lo, hi in rows[:, 1:3] for p in range(lo, hi)]
+        rows = sorted((int(k), int(e)) for rr, k, e, n in work if rr == r)
+        assert all(n == nchunks[r] for rr, _, _, n in work if rr == r)
+        assert [k for k, _ in rows] == list(range(nchunks[r]))
+        covered = [p for k, e in rows for p in range(k * cp, e)]
         assert covered == list(range(npages[r]))
     # locations: (last page, last_page_len - 1); (-1, -1) for a request without pages
     exp = []

@@ -164,7 +164,7 @@ def test_pages_are_conserved_through_alloc_and_free():
 
 def test_split_chunks_cover_every_page_once():
     kv_indptr = np.array([0, 0, 3, 40, 41, 300])
-    cp, n = P.split_chunks(kv_indptr, 16, 64, 4)
+    cp, n = P.split_chunks(kv_indptr, 16, 64, 4, min_chunk_tokens=256)
     assert cp == max(16, -(-300 // 16))
     pages = np.diff(kv_indptr)
     for npg, k in zip(pages, n):
