@@ -39,7 +39,23 @@ from mstar_amd.cache_manager import BatchedCacheManager, WorkspaceBufferManager 
 from mstar_amd.kv_store import KVCacheConfig, PagedAllocationManager  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per decode launch measured by rocprofv3 --pmc (FETCH_SIZE and
+# WRITE_SIZE passes scaled by a copy-kernel calibration); the summary that
+# holds the figure is regenerated whenever the decode kernel changes.
+TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "decode_kernel_c3_pmc.md")
 METRIC = "paged decode attn tokens/s + achieved HBM GB/s (% peak), 1 MI355X, B=256"
+
+
+def measured_traffic() -> int | None:
+    """``traffic_bytes_per_launch`` from the committed rocprofv3 --pmc summary, or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
 
 
 def _log(msg: str) -> None:
@@ -273,7 +289,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "decode_kernel",
             "kernel_us": dec_s * 1e6,
             "algorithmic_bytes": int(np.mean(bytes_per)),

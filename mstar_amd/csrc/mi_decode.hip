@@ -46,14 +46,17 @@ constexpr int kRows = 16;             // MFMA N: query rows per wave
 constexpr int kMinChunkTokens = 1024;  // never split a request finer than this (4 waves x 256)
 
 
-// Target number of wavefronts for one plan: ~8K (item, kv-head, quarter)
-// wave units keeps 256 CUs x 4 SIMDs busy with a short tail.
+// Target number of wavefronts for one plan: ~4K (item, kv-head, quarter)
+// wave units fill 256 CUs x 2 resident workgroups about twice; with the
+// longest-first work order the drain tail stays short while few requests
+// need partials (measured on c3: 4096 -> 545 us, 8192 -> 558 us,
+// 16384 -> 586 us).
 // MSTAR_DECODE_TARGET_UNITS overrides it for tuning sweeps (read once per
 // process).
 static int32_t decode_target_units() {
   static const int32_t units = [] {
     const char* e = getenv("MSTAR_DECODE_TARGET_UNITS");
-    int v = e ? atoi(e) : 8192;
+    int v = e ? atoi(e) : 4096;
     return v < 64 ? 64 : v;
   }();
   return units;

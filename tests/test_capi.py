@@ -1,0 +1,91 @@
+"""The C-ABI library without a GPU: it loads, exports every function that
+``include/mstar_amd.h`` declares with the argument count the ctypes binding
+uses, sizes workspaces on the host, and rejects invalid arguments before any
+HIP call (every call below returns from argument validation, so none touches
+a device).
+"""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from mstar_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mstar_amd.h"
+
+MI_ERR_INVALID = -1
+MI_ERR_UNSUPPORTED = -2
+
+
+def _declared():
+    """name -> number of parameters, from the prototypes in the header."""
+    text = re.sub(r"/\*.*?\*/|//[^\n]*", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(mi_[a-z0-9_]+)\s*\(([^;{)]*)\)\s*;", text):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+@pytest.fixture(scope="module")
+def L():
+    return _lib.lib()
+
+
+def test_header_declares_the_bound_functions():
+    decl = _declared()
+    assert set(decl) == set(_lib.SIGNATURES)
+    for name, nargs in decl.items():
+        assert len(_lib.SIGNATURES[name][1]) == nargs, name
+
+
+def test_library_exports_every_declared_symbol(L):
+    res = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True)
+    exported = {ln.split()[-1] for ln in res.stdout.splitlines() if ln.strip()}
+    for name in _declared():
+        assert name in exported, name
+        assert getattr(L, name) is not None
+
+
+def test_abi_version_and_status_strings(L):
+    assert L.mi_abi_version() == _lib.ABI_VERSION
+    for code, text in [(0, b"ok"), (-1, b"invalid argument")]:
+        assert L.mi_status_string(code) == text
+    for code in (-2, -3, -4, 12345):
+        assert L.mi_status_string(code)
+
+
+def test_workspace_sizes_are_host_arithmetic(L):
+    d = L.mi_decode_workspace_bytes(256, 32, 4, 128)
+    assert d > 0 and d % 256 == 0
+    # per item the workspace holds at least the fp32 partial output of every kv-head
+    assert d >= 256 * 4 * 16 * 128 * 4
+    assert L.mi_decode_workspace_bytes(512, 32, 4, 128) > d
+    p = L.mi_prefill_workspace_bytes(8, 4096, 32, 4, 128)
+    assert p > 0 and p % 256 == 0
+    assert L.mi_prefill_workspace_bytes(8, 8192, 32, 4, 128) > p
+    assert L.mi_decode_workspace_bytes(-1, 32, 4, 128) < 0
+    assert L.mi_prefill_workspace_bytes(8, 4096, 32, 5, 128) < 0  # 32 % 5 != 0
+
+
+def test_invalid_arguments_are_rejected_before_launch(L):
+    nul = None
+    # negative batch, null outputs
+    assert L.mi_pack(nul, nul, nul, nul, -1, nul, 0, 16, nul, nul, nul, nul, nul, 1, nul) == MI_ERR_INVALID
+    assert L.mi_block_table_update(nul, 0, nul, nul, nul, 4, nul) == MI_ERR_INVALID
+    # null workspace
+    assert L.mi_decode_plan(nul, nul, nul, nul, 4, 16, 32, 4, 128, nul, nul, 0, nul) == MI_ERR_INVALID
+
+
+def test_unsupported_shapes_are_reported(L):
+    buf = (ctypes.c_int32 * 8)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    # GQA group 32 > 16 rows per wavefront, page size not a multiple of 16, head_dim 96
+    assert L.mi_decode_plan(p, p, p, p, 1, 16, 32, 1, 128, None, p, 1 << 30, None) == MI_ERR_UNSUPPORTED
+    assert L.mi_decode_plan(p, p, p, p, 1, 8, 32, 4, 128, None, p, 1 << 30, None) == MI_ERR_UNSUPPORTED
+    assert L.mi_decode_plan(p, p, p, p, 1, 16, 32, 4, 96, None, p, 1 << 30, None) == MI_ERR_UNSUPPORTED
+

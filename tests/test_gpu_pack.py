@@ -87,7 +87,7 @@ def test_pack_allocation_failure_is_raised_before_launch(gpu):
     assert len(mgr.get_state("a", "main").page_indices) == 7  # earlier request keeps its pages
 
 
-def _split_layout(batch, nkv, d, units=8192):
+def _split_layout(batch, nkv, d, units=4096):
     target = max(16, units // (4 * nkv))
     max_chunks = target + batch  # the workspace below is large enough for the full budget
     align = lambda x: (x + 255) // 256 * 256
@@ -112,7 +112,7 @@ def test_decode_plan_partition(gpu):
     torch.cuda.synchronize()
     hdr, ci, wk, max_chunks = _split_layout(len(lens), hkv, d)
     h = ws[hdr:hdr + 20].cpu().view(torch.int32).tolist()
-    cp, nchunks = P.split_chunks(kv_indptr, 16, 8192, hkv)
+    cp, nchunks = P.split_chunks(kv_indptr, 16, 4096, hkv)
     assert h[0] == 0x4D494450 and h[1] == len(lens) and h[3] == cp and h[2] == int(nchunks.sum())
     cptr = ws[ci:ci + 4 * (len(lens) + 1)].cpu().view(torch.int32).numpy()
     assert cptr.tolist() == [0] + np.cumsum(nchunks).tolist()
