@@ -42,14 +42,15 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per decode launch measured by rocprofv3 --pmc (FETCH_SIZE and
 # WRITE_SIZE passes scaled by a copy-kernel calibration); the summary that
 # holds the figure is regenerated whenever the decode kernel changes.
-TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "decode_kernel_c3_pmc.md")
+TRAFFIC_PROFILE = os.path.join(REPO, "profiles", "decode_kernel_{config}_pmc.md")
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 METRIC = "paged decode attn tokens/s + achieved HBM GB/s (% peak), 1 MI355X, B=256"
 
 
-def measured_traffic() -> int | None:
+def measured_traffic(config: str) -> int | None:
     """``traffic_bytes_per_launch`` from the committed rocprofv3 --pmc summary, or None."""
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(TRAFFIC_PROFILE.format(config=config)) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     return int(line.split(":", 1)[1].strip())
@@ -62,6 +63,36 @@ def _log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def fill_pool(kv: torch.Tensor, spec, device: torch.device):
+    """N(0,1) K/V drawn in bf16 from a seeded device generator.
+
+    An fp8 pool is quantised per (K|V, kv-head) with s = amax/448 over the
+    whole pool (two passes over the same draws); returns the fp32 scales
+    ``[1, 2, num_kv_heads]`` or None for a bf16 pool.
+    """
+    gen = torch.Generator(device=device).manual_seed(spec.seed)
+    chunk = 1 << 14
+    pages = kv.shape[1]
+    if kv.dtype != torch.float8_e4m3fn:
+        for p0 in range(0, pages, chunk):
+            kv[0, p0:p0 + chunk].normal_(generator=gen)
+        return None
+    tmp = torch.empty((chunk,) + tuple(kv.shape[2:]), dtype=torch.bfloat16, device=device)
+    amax = torch.zeros(2, spec.num_kv_heads, device=device)
+    state = gen.get_state()
+    for p0 in range(0, pages, chunk):
+        t = tmp[:min(chunk, pages - p0)].normal_(generator=gen)
+        amax = torch.maximum(amax, t.abs().amax(dim=(0, 2, 4)).float())
+    scales = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    inv = (1.0 / scales).view(1, 2, 1, spec.num_kv_heads, 1)
+    gen.set_state(state)
+    for p0 in range(0, pages, chunk):
+        n = min(chunk, pages - p0)
+        t = tmp[:n].normal_(generator=gen)
+        kv[0, p0:p0 + n] = (t.float() * inv).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return scales.view(1, 2, spec.num_kv_heads).contiguous()
+
+
 def setup(spec_name: str, device: torch.device):
     bt = S.make_batch(spec_name)
     s = bt.spec
@@ -69,12 +100,9 @@ def setup(spec_name: str, device: torch.device):
     cfg = KVCacheConfig(num_layers=1, num_kv_heads=s.num_kv_heads, head_dim=s.head_dim,
                         max_seq_len=40960, max_num_pages=s.pool_pages, page_size=s.page_size,
                         num_qo_heads=s.num_qo_heads)
-    kv = torch.empty(1, s.pool_pages, 2, s.page_size, s.num_kv_heads, s.head_dim, dtype=torch.bfloat16,
-                     device=device)
-    gen = torch.Generator(device=device).manual_seed(s.seed)
-    chunk = 1 << 14
-    for p0 in range(0, s.pool_pages, chunk):
-        kv[0, p0:p0 + chunk].normal_(generator=gen)
+    kv_dtype = torch.float8_e4m3fn if s.kv_dtype == "fp8" else torch.bfloat16
+    kv = torch.empty(1, s.pool_pages, 2, s.page_size, s.num_kv_heads, s.head_dim, dtype=kv_dtype, device=device)
+    scales = fill_pool(kv, s, device)
     mgr = PagedAllocationManager(cfg, kv, device=device)
     # Steady state: each request already holds its T-1 cached tokens on the
     # drawn (random) pages; the allocator's free list holds the rest of the
@@ -92,7 +120,7 @@ def setup(spec_name: str, device: torch.device):
         st.seq_len = int(bt.kv_len[i]) - 1
         st.position_id_start = st.seq_len
     bufs = WorkspaceBufferManager(512 << 20, device)  # the reference's per-label workspace size
-    cm = BatchedCacheManager(rids, {r: "main" for r in rids}, kv, mgr, bufs, cfg, device)
+    cm = BatchedCacheManager(rids, {r: "main" for r in rids}, kv, mgr, bufs, cfg, device, kv_scales=scales)
     g = torch.Generator().manual_seed(s.seed + 1)
     q = torch.randn(b, s.num_qo_heads, s.head_dim, generator=g).to(torch.bfloat16).to(device)
     k = torch.randn(b, s.num_kv_heads, s.head_dim, generator=g).to(torch.bfloat16).to(device)
@@ -103,42 +131,52 @@ def setup(spec_name: str, device: torch.device):
 def decode_bytes(seq_lens_after: np.ndarray, total_pages: int, s) -> int:
     """Algorithmic HBM bytes of one decode-kernel launch (partials excluded)."""
     b = len(seq_lens_after)
-    kv = int(seq_lens_after.sum()) * s.num_kv_heads * s.head_dim * 2 * 2
+    elem = 1 if s.kv_dtype == "fp8" else 2
+    kv = int(seq_lens_after.sum()) * s.num_kv_heads * s.head_dim * 2 * elem
     qo = b * s.num_qo_heads * s.head_dim * 2 * 2
     idx = 4 * (total_pages + 3 * b)
-    return kv + qo + idx
+    scales = 2 * s.num_kv_heads * 4 if elem == 1 else 0
+    return kv + qo + idx + scales
+
+
+def _layer_scales(cm):
+    if cm.kv_scales is None:
+        return None, None
+    return cm.kv_scales[0, 0], cm.kv_scales[0, 1]
 
 
 def step_once(cm, q, k, v, b, events=None):
     cm.plan_attention([1] * b)
     wrapper = cm._plan_states["main"].wrapper
     layer = cm.kv_cache[0]
-    wrapper.set_kv_cache(layer, k, v)
+    ks, vs = _layer_scales(cm)
+    wrapper.set_kv_cache(layer, k, v, k_scale=ks, v_scale=vs)
     if events is None:
-        out = wrapper.run(q, layer)
+        out = wrapper.run(q, layer, k_scale=ks, v_scale=vs)
     else:
-        out = _run_split(wrapper, q, layer, events)
+        out = _run_split(wrapper, q, layer, ks, vs, events)
     cm.advance_seq_lens()
     return out
 
 
-def _run_split(w, q, layer, events):
+def _run_split(w, q, layer, ks, vs, events):
     """wrapper.run() as its two C entry points, with HIP events around the decode kernel."""
-    desc = _lib.paged_kv_desc(layer)
+    desc = _lib.paged_kv_desc(layer, ks, vs)
     out = torch.empty_like(q)
     args = (q.data_ptr(), _lib.MI_BF16, q.stride(0), q.stride(1), desc, None, w._indptr.data_ptr(),
             w._indices.data_ptr(), w._last.data_ptr(), w._n_req, w.num_qo_heads, 0, 1.0 / math.sqrt(w.head_dim),
             w._workspace.data_ptr(), w._workspace.numel(), out.data_ptr(), out.stride(0), out.stride(1),
             _lib.stream_ptr(q.device))
-    e0, e1 = events
+    e0, e1, e2 = events
     e0.record()
     _lib.check(_lib.lib().mi_decode_attend(*args), "mi_decode_attend")
     e1.record()
     _lib.check(_lib.lib().mi_decode_merge(*args), "mi_decode_merge")
+    e2.record()
     return out
 
 
-def cpu_baseline(bt, kv_gpu, q, k, v, budget_s: float = 12.0):
+def cpu_baseline(bt, kv_gpu, q, k, v, scales=None, budget_s: float = 12.0):
     """The CPU restatement (oracle/) on a sample of the batch: pack + append + fp32 attention."""
     from oracle import attention as A
     from oracle import packing as P
@@ -154,6 +192,9 @@ def cpu_baseline(bt, kv_gpu, q, k, v, budget_s: float = 12.0):
     cache = kv_gpu[0, torch.as_tensor(uniq, device=kv_gpu.device)].cpu()
     idx = np.asarray([remap[int(p)] for p in pages], dtype=np.int32)
     qc, kc, vc = q[:nreq].cpu(), k[:nreq].cpu(), v[:nreq].cpu()
+    ks = vs = None
+    if scales is not None:
+        ks, vs = scales[0, 0].cpu(), scales[0, 1].cpu()
     times = []
     t_end = time.perf_counter() + budget_s
     while time.perf_counter() < t_end or len(times) < 3:
@@ -169,8 +210,9 @@ def cpu_baseline(bt, kv_gpu, q, k, v, budget_s: float = 12.0):
         pool.free.extend(extra)
         packed = P.pack(states, [1] * nreq, pool, s.page_size)
         loc = packed.kv_locations
-        A.append(cache, loc[:, 0], loc[:, 1], kc, vc)
-        A.paged_attention(qc, cache, None, packed.kv_indptr, packed.kv_indices, packed.last_page_len, causal=False)
+        A.append(cache, loc[:, 0], loc[:, 1], kc, vc, ks, vs)
+        A.paged_attention(qc, cache, None, packed.kv_indptr, packed.kv_indices, packed.last_page_len, causal=False,
+                          k_scale=ks, v_scale=vs)
         times.append(time.perf_counter() - t0)
         if len(times) >= 10 and time.perf_counter() > t_end:
             break
@@ -189,7 +231,7 @@ def cpu_baseline(bt, kv_gpu, q, k, v, budget_s: float = 12.0):
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"first {nreq} of the {len(bt.kv_len)} c3 requests ({int(sub.kv_len.sum())} KV tokens), "
+        "sample": (f"first {nreq} of the {len(bt.kv_len)} {s.name} requests ({int(sub.kv_len.sum())} KV tokens), "
                    f"pack + append + fp32 paged attention, median of {len(times)} runs, "
                    f"{threads} host threads, CPU: {model}"),
     }
@@ -213,26 +255,19 @@ def copy_calibration(dev) -> int:
     return 0
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c3")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run a plain device copy of 1 GiB (3x): the reference point that scales "
-                         "rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
-              file=sys.stderr)
-        return 2
-    dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
-    if args.copy_calibration:
-        return copy_calibration(dev)
-    _lib.lib()
+WORKLOADS = {
+    "c2": "c2: Orpheus (Llama-3.2-3B) decode, one layer-step of pack+plan+append+decode+merge",
+    "c3": "c3: Qwen3-Omni thinker decode, one layer-step of pack+plan+append+decode+merge",
+    "c4": "c4: BAGEL (Qwen2.5-7B) ragged chunked prefill + decode mix, one layer-step of plan+append+attention",
+    "c5": "c5: Qwen3-Omni thinker decode on an fp8-e4m3 KV cache, one layer-step of pack+plan+append+decode+merge",
+}
+
+
+def _kernel_events(n: int, k: int):
+    return [tuple(torch.cuda.Event(enable_timing=True) for _ in range(k)) for _ in range(n)]
+
+
+def bench_decode(args, dev) -> dict:
     _log(f"setup {args.config} ...")
     bt, cfg, kv, mgr, cm, rids, q, k, v = setup(args.config, dev)
     s = bt.spec
@@ -252,21 +287,132 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / args.steps
 
-    # timed region 2: same steps, decode kernel bracketed by HIP events
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # timed region 2: same steps, decode and merge kernels bracketed by HIP events
+    evs = _kernel_events(args.steps, 3)
     bytes_per = []
     for i in range(args.steps):
         seq_after = np.array([cm._get_state(r).seq_len + 1 for r in rids])
         step_once(cm, q, k, v, b, events=evs[i])
         bytes_per.append(decode_bytes(seq_after, sum(len(cm._get_state(r).page_indices) for r in rids), s))
     torch.cuda.synchronize()
-    dec_ms = np.array([a.elapsed_time(bb) for a, bb in evs])
+    dec_ms = np.array([e0.elapsed_time(e1) for e0, e1, _ in evs])
+    dm_ms = np.array([e0.elapsed_time(e2) for e0, _, e2 in evs])
     dec_s = float(dec_ms.mean()) / 1e3
     achieved = float(np.mean(bytes_per)) / dec_s / 1e9
     kv_tokens = int(sum(cm._get_state(r).seq_len for r in rids))
+    lo, hi = s.ctx[1], s.ctx[2]
     res = {
-        "metric": METRIC,
+        "metric": METRIC if s.name == "c3" else f"paged decode attn tokens/s + achieved HBM GB/s, 1 MI355X, B={b}",
         "value": b / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 KV, bf16 q/o, fp32 accumulate" if s.kv_dtype == "fp8" else "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": WORKLOADS[s.name],
+            "batch": b, "num_qo_heads": s.num_qo_heads, "num_kv_heads": s.num_kv_heads, "head_dim": s.head_dim,
+            "page_size": s.page_size, "context": f"{s.ctx[0]} [{lo}, {hi}]", "kv_pool_pages": s.pool_pages,
+            "kv_dtype": s.kv_dtype, "kv_tokens_at_end": kv_tokens,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": measured_traffic(s.name),
+            "kernel": "decode_kernel",
+            "kernel_us": dec_s * 1e6,
+            "kernel_us_median": float(np.median(dec_ms)) * 1e3,
+            "decode_plus_merge_us": float(dm_ms.mean()) * 1e3,
+            "algorithmic_bytes": int(np.mean(bytes_per)),
+        },
+    }
+    if not args.no_cpu_baseline:
+        _log("cpu baseline ...")
+        res["cpu_baseline"] = cpu_baseline(bt, kv, q, k, v, cm.kv_scales)
+    return res
+
+
+def prefill_flops(bt) -> tuple[int, int]:
+    """(flops of the MFMA-tile requests, flops of the short-query requests) of one causal step.
+
+    4*D*Hq flops per visible (query, key) pair: q.k and p.v, a multiply-add each.
+    Requests with qo_len*G <= 16 rows run on the decode kernel.
+    """
+    s = bt.spec
+    g = s.num_qo_heads // s.num_kv_heads
+    long_f = short_f = 0
+    for kvl, qo in zip(bt.kv_len.tolist(), bt.new_len.tolist()):
+        pairs = qo * (kvl - qo) + qo * (qo + 1) // 2
+        f = 4 * s.head_dim * s.num_qo_heads * pairs
+        if qo * g > 16:
+            long_f += f
+        else:
+            short_f += f
+    return long_f, short_f
+
+
+def bench_prefill(args, dev) -> dict:
+    from mstar_amd.paged_attention import PagedPrefillWrapper
+
+    _log(f"setup {args.config} ...")
+    bt = S.make_batch(args.config)
+    s = bt.spec
+    b = len(bt.kv_len)
+    ntok = bt.total_q_tokens
+    kv = torch.empty(1, s.pool_pages, 2, s.page_size, s.num_kv_heads, s.head_dim, dtype=torch.bfloat16, device=dev)
+    fill_pool(kv, s, dev)
+    layer = kv[0]
+    g = torch.Generator().manual_seed(s.seed + 1)
+    q = torch.randn(ntok, s.num_qo_heads, s.head_dim, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(ntok, s.num_kv_heads, s.head_dim, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(ntok, s.num_kv_heads, s.head_dim, generator=g).to(torch.bfloat16).to(dev)
+    ws = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    w = PagedPrefillWrapper(ws, s.num_qo_heads, s.num_kv_heads, s.head_dim, s.page_size, device=dev)
+    meta = [torch.from_numpy(a) for a in (bt.qo_indptr, bt.kv_indptr, bt.kv_indices, bt.last_page_len)]
+
+    def step(events=None):
+        w.plan(*meta, causal=True)
+        w.set_kv_cache(layer, k, v)
+        if events is None:
+            return w.run(q, layer)
+        return _prefill_split(w, q, layer, events)
+
+    torch.cuda.synchronize()
+    _log(f"warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    evs = _kernel_events(args.steps, 3)
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    tile_ms = np.array([e1.elapsed_time(e2) for _, e1, e2 in evs])
+    short_ms = np.array([e0.elapsed_time(e1) for e0, e1, _ in evs])
+    long_f, short_f = prefill_flops(bt)
+    tile_s = float(tile_ms.mean()) / 1e3
+    achieved = long_f / tile_s / 1e12
+    short_bytes = 0
+    g_ = s.num_qo_heads // s.num_kv_heads
+    for kvl, qo in zip(bt.kv_len.tolist(), bt.new_len.tolist()):
+        if qo * g_ <= 16:
+            short_bytes += kvl * s.num_kv_heads * s.head_dim * 2 * 2 + qo * s.num_qo_heads * s.head_dim * 2 * 2
+    return {
+        "metric": "ragged prefill+decode attn tokens/s + prefill MFMA TFLOP/s, 1 MI355X",
+        "value": ntok / wall,
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -278,26 +424,70 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": f"{s.name}: Qwen3-Omni thinker decode, one layer-step of pack+plan+append+decode+merge",
-            "batch": b, "num_qo_heads": s.num_qo_heads, "num_kv_heads": s.num_kv_heads, "head_dim": s.head_dim,
-            "page_size": s.page_size, "context": "log-uniform [512, 32768]", "kv_pool_pages": s.pool_pages,
-            "kv_tokens_at_end": kv_tokens,
+            "workload": WORKLOADS[s.name],
+            "batch": b, "prefill_chunks": s.prefill_chunks, "q_tokens": ntok, "kv_tokens": bt.total_kv_tokens,
+            "num_qo_heads": s.num_qo_heads, "num_kv_heads": s.num_kv_heads, "head_dim": s.head_dim,
+            "page_size": s.page_size, "causal": True,
         },
         "roofline": {
-            "bound": "hbm",
+            "bound": "mfma",
             "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": measured_traffic(),
-            "kernel": "decode_kernel",
-            "kernel_us": dec_s * 1e6,
-            "algorithmic_bytes": int(np.mean(bytes_per)),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
+            "traffic": None,
+            "kernel": "prefill_kernel",
+            "kernel_us": tile_s * 1e6,
+            "kernel_us_median": float(np.median(tile_ms)) * 1e3,
+            "algorithmic_flops": long_f,
+            "short_query_part": {"kernels": "decode_kernel + merge_kernel", "us": float(short_ms.mean()) * 1e3,
+                                 "algorithmic_bytes": short_bytes,
+                                 "GBps": short_bytes / (float(short_ms.mean()) * 1e-3) / 1e9},
         },
     }
-    if not args.no_cpu_baseline:
-        _log("cpu baseline ...")
-        res["cpu_baseline"] = cpu_baseline(bt, kv, q, k, v)
+
+
+def _prefill_split(w, q, layer, events):
+    """wrapper.run() as its two C entry points, with HIP events around each."""
+    desc = _lib.paged_kv_desc(layer)
+    out = torch.empty_like(q)
+    args = (q.data_ptr(), _lib.MI_BF16, q.stride(0), q.stride(1), desc, w._qo.data_ptr(), w._indptr.data_ptr(),
+            w._indices.data_ptr(), w._last.data_ptr(), w._plan_batch, w._plan_max_tokens, w.num_qo_heads, 1,
+            1.0 / math.sqrt(w.head_dim), w._workspace.data_ptr(), w._workspace.numel(), out.data_ptr(),
+            out.stride(0), out.stride(1), _lib.stream_ptr(q.device))
+    e0, e1, e2 = events
+    e0.record()
+    _lib.check(_lib.lib().mi_prefill_short(*args), "mi_prefill_short")
+    e1.record()
+    _lib.check(_lib.lib().mi_prefill_tiles(*args), "mi_prefill_tiles")
+    e2.record()
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain device copy of 1 GiB (3x): the reference point that scales "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        return copy_calibration(dev)
+    _lib.lib()
+    if S.SPECS[args.config].prefill_chunks:
+        res = bench_prefill(args, dev)
+    else:
+        res = bench_decode(args, dev)
     print(json.dumps(res), flush=True)
     return 0
 

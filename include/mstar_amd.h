@@ -185,6 +185,11 @@ int mi_kv_append(const mi_paged_kv* kv, const void* k, const void* v, int32_t sr
  * mi_prefill_run replaces FlashInferPrefillWrapper.run (:258-269):
  *   out[t, h] = softmax(sm_scale * q[t,h] . K_r^T) V_r over the request's keys
  *   i <= kv_len - qo_len + j for query j (causal) or all kv_len keys.
+ * mi_prefill_run = mi_prefill_short (the short-query requests, through the
+ * split-KV decode kernel and merge) followed by mi_prefill_tiles (the MFMA
+ * tiles of the long-query requests).  The halves take the same arguments and
+ * write disjoint output rows; after the plan they may run in either order or
+ * on two streams.  They have no separate counterpart in the reference.
  * ------------------------------------------------------------------------ */
 int64_t mi_prefill_workspace_bytes(int32_t batch, int32_t max_qo_tokens, int32_t num_qo_heads,
                                    int32_t num_kv_heads, int32_t head_dim);
@@ -200,6 +205,18 @@ int mi_prefill_run(const void* q, int32_t q_dtype, int64_t q_stride_token, int64
                    int32_t max_qo_tokens, int32_t num_qo_heads, int32_t causal, float sm_scale, void* workspace,
                    int64_t workspace_bytes, void* out, int64_t out_stride_token,
                    int64_t out_stride_head, void* stream);
+int mi_prefill_short(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                     const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                     const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                     int32_t max_qo_tokens, int32_t num_qo_heads, int32_t causal, float sm_scale,
+                     void* workspace, int64_t workspace_bytes, void* out, int64_t out_stride_token,
+                     int64_t out_stride_head, void* stream);
+int mi_prefill_tiles(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                     const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                     const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                     int32_t max_qo_tokens, int32_t num_qo_heads, int32_t causal, float sm_scale,
+                     void* workspace, int64_t workspace_bytes, void* out, int64_t out_stride_token,
+                     int64_t out_stride_head, void* stream);
 
 #ifdef __cplusplus
 }

@@ -96,6 +96,16 @@ SIGNATURES = {
         [_P, _I32, _I64, _I64, ctypes.POINTER(MiPagedKV), _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32,
          _P, _I64, _P, _I64, _I64, _P],
     ),
+    "mi_prefill_short": (
+        ctypes.c_int,
+        [_P, _I32, _I64, _I64, ctypes.POINTER(MiPagedKV), _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32,
+         _P, _I64, _P, _I64, _I64, _P],
+    ),
+    "mi_prefill_tiles": (
+        ctypes.c_int,
+        [_P, _I32, _I64, _I64, ctypes.POINTER(MiPagedKV), _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32,
+         _P, _I64, _P, _I64, _I64, _P],
+    ),
 }
 
 _lock = threading.Lock()

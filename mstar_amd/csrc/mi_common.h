@@ -21,6 +21,9 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(4))) short i16x4;
 typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 
 // ---------------------------------------------------------------- bit casts
 template <typename To, typename From>
@@ -77,7 +80,8 @@ struct BF16 {
   MI_DEVICE static uint16_t from_f32(float x) { return f32_to_bf16_rne(x); }
   // Two floats -> packed pair, RNE (hardware v_cvt_pk_bf16_f32 on gfx950).
   MI_DEVICE static uint32_t pack2(float a, float b) {
-    return (uint32_t)bitcast<uint16_t>((__bf16)a) | ((uint32_t)bitcast<uint16_t>((__bf16)b) << 16);
+    const f32x2 v = {a, b};
+    return bitcast<uint32_t>(__builtin_convertvector(v, bf16x2));
   }
   // S^T tile product: A = 16x32 (8 elems/lane), B = 32x16, C = 16x16 fp32.
   MI_DEVICE static f32x4 mma_16x16x32(const uint4& a, const uint4& b, f32x4 c) {
@@ -87,20 +91,30 @@ struct BF16 {
   MI_DEVICE static f32x4 mma_16x16x16(const uint2& a, const uint2& b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bitcast<i16x4>(a), bitcast<i16x4>(b), c, 0, 0, 0);
   }
+  // acc + lo(w) + hi(w) of a packed pair, in one v_dot2.
+  MI_DEVICE static float sum2(uint32_t w, float acc) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(w), one, acc, false);
+  }
 };
 
 struct F16 {
   static constexpr int kDtype = MI_F16;
   MI_DEVICE static float to_f32(uint16_t h) { return f16_to_f32(h); }
   MI_DEVICE static uint16_t from_f32(float x) { return f32_to_f16_rne(x); }
-  MI_DEVICE static uint32_t pack2(float a, float b) {
-    return (uint32_t)bitcast<uint16_t>((_Float16)a) | ((uint32_t)bitcast<uint16_t>((_Float16)b) << 16);
+  MI_DEVICE static uint32_t pack2(float a, float b) {  // v_cvt_pk_f16_f32, RNE
+    const f32x2 v = {a, b};
+    return bitcast<uint32_t>(__builtin_convertvector(v, f16x2));
   }
   MI_DEVICE static f32x4 mma_16x16x32(const uint4& a, const uint4& b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<f16x8>(a), bitcast<f16x8>(b), c, 0, 0, 0);
   }
   MI_DEVICE static f32x4 mma_16x16x16(const uint2& a, const uint2& b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(bitcast<f16x4>(a), bitcast<f16x4>(b), c, 0, 0, 0);
+  }
+  MI_DEVICE static float sum2(uint32_t w, float acc) {
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(bitcast<f16x2>(w), one, acc, false);
   }
 };
 

@@ -29,7 +29,12 @@
 
 namespace mi {
 
-constexpr int kTileRows = 128;  // rows per workgroup
+// Wavefronts per prefill workgroup (32 rows each): 8 (two per SIMD) while
+// the per-wave state fits 256 registers, 4 for head_dim 256.
+constexpr int pf_waves(int head_dim) { return head_dim > 128 ? 4 : 8; }
+constexpr int pf_rows(int head_dim) { return 32 * pf_waves(head_dim); }  // (token, q-head) rows per workgroup
+constexpr int kPfKeys = 32;                // keys per K/V tile
+constexpr int kPfPageCap = 2048;           // page ids staged in LDS at a time
 constexpr int kShortRows = 16;  // qo_len * group <= 16 -> decode kernel
 
 struct PrefillLayout {
@@ -37,10 +42,11 @@ struct PrefillLayout {
   int32_t max_tiles;
 };
 
-static PrefillLayout prefill_layout(int32_t batch, int32_t max_qo_tokens, int32_t group) {
+static PrefillLayout prefill_layout(int32_t batch, int32_t max_qo_tokens, int32_t group, int32_t head_dim) {
+  const int tile_rows = pf_rows(head_dim);
   PrefillLayout L;
   const int64_t rows = (int64_t)max_qo_tokens * group;
-  int64_t mt = (rows + kTileRows - 1) / kTileRows + batch;
+  int64_t mt = (rows + tile_rows - 1) / tile_rows + batch;
   if (mt > (1 << 28)) mt = 1 << 28;
   L.max_tiles = (int32_t)mt;
   L.hdr = 0;
@@ -83,7 +89,8 @@ __global__ __launch_bounds__(256) void token_map_kernel(const int32_t* qo_indptr
 
 // ------------------------------------------------------------ tile plan
 __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* qo_indptr, int32_t batch,
-                                                            int32_t group, int32_t max_tiles, int32_t* hdr,
+                                                            int32_t group, int32_t tile_rows, int32_t max_tiles,
+                                                            int32_t* hdr,
                                                             int2* tiles) {
   __shared__ int smem[16];
   int carry = 0;
@@ -92,12 +99,12 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* qo_in
     int n = 0;
     if (b < batch) {
       const int rows = (qo_indptr[b + 1] - qo_indptr[b]) * group;
-      n = rows > kShortRows ? (rows + kTileRows - 1) / kTileRows : 0;
+      n = rows > kShortRows ? (rows + tile_rows - 1) / tile_rows : 0;
     }
     int total;
     const int first = block_exclusive_scan_1024(n, total, smem) + carry;
     for (int i = 0; i < n && first + i < max_tiles; ++i)
-      tiles[first + i] = make_int2(b, (n - 1 - i) * kTileRows);  // causal: heaviest tile first
+      tiles[first + i] = make_int2(b, (n - 1 - i) * tile_rows);  // causal: heaviest tile first
     carry += total;
   }
   if (threadIdx.x == 0) hdr[0] = min(carry, max_tiles);
@@ -125,23 +132,28 @@ struct PrefillParams {
 
 template <typename MT, bool FP8, int D>
 struct PrefillCfg {
-  static constexpr int KEYS = D > 128 ? 32 : 64;          // keys per LDS tile
-  static constexpr int RS = D * 2 + 16;                   // LDS row stride (bytes, 16-bit elements)
-  static constexpr int ESZ = FP8 ? 1 : 2;                 // cache element size
-  static constexpr int CPR = D * ESZ / 16;                // 16-byte chunks per cached row
-  static constexpr int RPP = 256 / CPR;                   // rows per loader pass
-  static constexpr int NP = KEYS / RPP;                   // loader passes per tile
-  static_assert(KEYS % RPP == 0, "loader mapping");
+  static constexpr int THREADS = 64 * pf_waves(D);
+  static constexpr int ROWS = pf_rows(D);
+  static constexpr int KEYS = kPfKeys;                     // keys per K/V tile
+  static constexpr int RS = D * 2 + 16;                    // LDS row stride (bytes, MFMA-type elements)
+  static constexpr int ESZ = FP8 ? 1 : 2;                  // cache element size
+  static constexpr int CPR = D * ESZ / 16;                 // 16-byte chunks per cached row
+  static constexpr int HALF = KEYS * CPR;                  // chunks of the K (or V) half of a tile
+  static constexpr int NL = (2 * HALF + THREADS - 1) / THREADS;  // loader chunks per thread
+  static constexpr int STAGE = 2 * KEYS * RS;              // one LDS stage: K rows then V rows
+  static_assert(HALF % 64 == 0, "a wavefront's loader chunks must stay in one half");
+  static_assert((2 * HALF) % THREADS == 0 || 2 * HALF < THREADS, "loader mapping");
 };
 
 template <typename MT, bool FP8, int D>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams p) {
   using C = PrefillCfg<MT, FP8, D>;
-  constexpr int KS = D / 32, VW = D / 16, KEYS = C::KEYS, RS = C::RS, ESZ = C::ESZ;
-  constexpr int NSUB = KEYS / 16;
+  constexpr int KS = D / 32, VW = D / 16, KEYS = C::KEYS, RS = C::RS, ESZ = C::ESZ, CPR = C::CPR;
+  constexpr int THREADS = C::THREADS, NL = C::NL, HALF = C::HALF, STAGE = C::STAGE;
+  constexpr int LCH = FP8 ? 32 : 16;  // LDS bytes per loaded chunk
   constexpr float kNegInf = -__builtin_inff();
-  __shared__ __attribute__((aligned(16))) uint8_t lds_k[KEYS * RS];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_v[KEYS * RS];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+  __shared__ int32_t lds_pages[kPfPageCap];
 
   // ---- XCD-aware unit: XCD x = blockIdx % 8 takes units [x*per, (x+1)*per)
   const int nkv = p.num_kv_heads;
@@ -176,7 +188,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
     const int n = row0 + 32 * wave + 16 * rg + col;
     const int tok = n / G, g = n - tok * G;
     const bool valid = n < rows_total;
-    int l = p.causal ? (kv_len - qo_len + tok) : (kv_len - 1);
+    const int l = p.causal ? (kv_len - qo_len + tok) : (kv_len - 1);
     lim[rg] = min(l, kv_len - 1);
     const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(qo_start + tok) * p.q_stride_tok +
                            (int64_t)(h * G + g) * p.q_stride_head;
@@ -185,7 +197,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
       qf[rg][s] = valid ? *(const uint4*)(qrow + 32 * s + 8 * grp) : make_uint4(0, 0, 0, 0);
   }
   // ---- keys this workgroup needs, and where per-row masking starts
-  const int last_row = min(row0 + kTileRows, rows_total) - 1;
+  const int last_row = min(row0 + C::ROWS, rows_total) - 1;
   const int max_tok = last_row / G, min_tok = row0 / G;
   const int kv_end = p.causal ? min(kv_len, kv_len - qo_len + max_tok + 1) : kv_len;
   const int mask_from = p.causal ? (kv_len - qo_len + min_tok + 1) : kv_len;
@@ -198,50 +210,67 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
   }
   const float sl2 = p.scale_log2 * kscale;
 
-  // ---- cooperative tile loader: thread -> (row tid / CPR + pass*RPP, chunk tid % CPR)
+  // ---- loader: chunk c = tid + i*THREADS -> (half, row, 16-byte column).
+  // A wavefront's 64 chunks of one load cover 64/CPR <= 16 consecutive rows
+  // of one half starting at a multiple of 64/CPR, so they lie in one
+  // 16-row group of keys and hence in one page (page_size is a multiple of
+  // 16, tiles start at multiples of 32): page and slot base are scalars.
   const uint8_t* kvb = (const uint8_t*)p.kv + (int64_t)h * p.head_stride * ESZ;
-  const int lrow = tid / C::CPR, lchunk = tid - lrow * C::CPR;
-  uint4 kreg[C::NP], vreg[C::NP];
-  auto load_tile = [&](int kt) {
+  const int64_t tok_bytes = p.token_stride * ESZ;
+  uint32_t l_off[NL];   // per-thread byte offset within (page, first slot of its group)
+  int l_grp[NL];        // first key row of the 16-row group (wave-uniform)
+  int l_row[NL];        // key row within the tile
+  bool l_v[NL];         // V half
 #pragma unroll
-    for (int i = 0; i < C::NP; ++i) {
-      const int key = kt * KEYS + i * C::RPP + lrow;
-      if (key < kv_end) {
-        const int page = p.kv_indices[page_base + key / ps];
-        const uint8_t* src = kvb + ((int64_t)page * p.page_stride + (int64_t)(key % ps) * p.token_stride) * ESZ +
-                             16 * lchunk;
-        kreg[i] = *(const uint4*)src;
-        vreg[i] = *(const uint4*)(src + p.kv_stride * ESZ);
-      } else {
-        kreg[i] = make_uint4(0, 0, 0, 0);
-        vreg[i] = make_uint4(0, 0, 0, 0);
+  for (int i = 0; i < NL; ++i) {
+    const int c = tid + i * THREADS;
+    const int half = c / HALF, rem = c - half * HALF;
+    const int row = rem / CPR, ch = rem - row * CPR;
+    l_row[i] = row;
+    l_grp[i] = uniform(row) & ~15;
+    l_v[i] = half == 1;
+    l_off[i] = (uint32_t)((int64_t)half * p.kv_stride * ESZ + (int64_t)(row - (row & ~15)) * tok_bytes + 16 * ch);
+  }
+  const int key_cap = np * ps - 16;  // last 16-row group inside the request's pages
+  uint4 ra[NL], rb[NL];
+  int c0 = 0;  // first page of the page ids staged in LDS
+  auto load_tile = [&](int t, uint4 (&r)[NL]) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      if (2 * HALF % THREADS == 0 || tid + i * THREADS < 2 * HALF) {
+        // groups past the request's last page re-read its last group (masked, V zeroed)
+        const int gkey = uniform(min(t * KEYS + l_grp[i], key_cap));
+        const int pabs = gkey / ps;
+        const int page = uniform(lds_pages[pabs - c0]);
+        const uint8_t* base = kvb + (int64_t)page * p.page_stride * ESZ + (int64_t)(gkey - pabs * ps) * tok_bytes;
+        r[i] = *(const uint4*)(base + l_off[i]);
       }
     }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](int t, const uint4 (&r)[NL], int stage) {
 #pragma unroll
-    for (int i = 0; i < C::NP; ++i) {
-      const int r = i * C::RPP + lrow;
-      if constexpr (FP8) {  // 16 fp8 -> 16 MFMA-type elements (32 bytes)
-        const uint32_t kw[4] = {kreg[i].x, kreg[i].y, kreg[i].z, kreg[i].w};
-        const uint32_t vw[4] = {vreg[i].x, vreg[i].y, vreg[i].z, vreg[i].w};
-        uint32_t ko[8], vo[8];
+    for (int i = 0; i < NL; ++i) {
+      const int c = tid + i * THREADS;
+      if (2 * HALF % THREADS == 0 || c < 2 * HALF) {
+        const int half = c / HALF, rem = c - half * HALF;
+        const int row = rem / CPR, ch = rem - row * CPR;
+        uint4 v = r[i];
+        // V rows past the KV end may hold anything (unwritten slots of the last page)
+        if (l_v[i] && t * KEYS + l_row[i] >= kv_len) v = make_uint4(0, 0, 0, 0);
+        uint8_t* dst = lds + stage * STAGE + half * KEYS * RS + row * RS + LCH * ch;
+        if constexpr (FP8) {  // 16 fp8 -> 16 MFMA-type elements (32 bytes)
+          const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+          uint32_t o[8];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          ko[2 * w] = fp8x2_to_mt<MT>(kw[w], false);
-          ko[2 * w + 1] = fp8x2_to_mt<MT>(kw[w], true);
-          vo[2 * w] = fp8x2_to_mt<MT>(vw[w], false);
-          vo[2 * w + 1] = fp8x2_to_mt<MT>(vw[w], true);
+          for (int k = 0; k < 4; ++k) {
+            o[2 * k] = fp8x2_to_mt<MT>(w[k], false);
+            o[2 * k + 1] = fp8x2_to_mt<MT>(w[k], true);
+          }
+          *(uint4*)dst = make_uint4(o[0], o[1], o[2], o[3]);
+          *(uint4*)(dst + 16) = make_uint4(o[4], o[5], o[6], o[7]);
+        } else {
+          *(uint4*)dst = v;
         }
-        uint8_t* kd = lds_k + r * RS + 32 * lchunk;
-        uint8_t* vd = lds_v + r * RS + 32 * lchunk;
-        *(uint4*)kd = make_uint4(ko[0], ko[1], ko[2], ko[3]);
-        *(uint4*)(kd + 16) = make_uint4(ko[4], ko[5], ko[6], ko[7]);
-        *(uint4*)vd = make_uint4(vo[0], vo[1], vo[2], vo[3]);
-        *(uint4*)(vd + 16) = make_uint4(vo[4], vo[5], vo[6], vo[7]);
-      } else {
-        *(uint4*)(lds_k + r * RS + 16 * lchunk) = kreg[i];
-        *(uint4*)(lds_v + r * RS + 16 * lchunk) = vreg[i];
       }
     }
   };
@@ -251,114 +280,136 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
   for (int rg = 0; rg < 2; ++rg)
 #pragma unroll
     for (int jj = 0; jj < VW; ++jj) acc[rg][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Running max in raw-score units.  It is raised only when a tile's max
+  // exceeds it by more than kLazy (exp2 units): probabilities then stay
+  // <= 2^kLazy, harmless in fp32 sums and bf16/fp16 P, and the O rescale
+  // is skipped on almost every tile.
+  constexpr float kLazy = 8.f;
+  const float lazy_raw = kLazy / sl2;
   float m_run[2] = {kNegInf, kNegInf}, l_run[2] = {0.f, 0.f};
 
-  auto compute = [&](int kt) {
-    const int kb = kt * KEYS;
-    // S^T for both row groups, NSUB sub-tiles of 16 keys
-    f32x4 s[2][NSUB];
+  // first tile that reaches past some row's limit: (t+1)*KEYS > mask_from
+  const int t_mask = mask_from > 0 ? mask_from / KEYS : 0;
+
+  // One 32-key tile: S^T = K.Q^T as two 16-key sub-tiles (16x16x32 MFMAs,
+  // K fragments from LDS shared by both row groups), online softmax, then
+  // O^T += V^T.P^T as one 16x16x32 MFMA per 16 output dims.  The MFMA k
+  // index i of lane group grp stands for key 4*grp+i (i < 4) or 16+4*grp+i-4
+  // (i >= 4): exactly the keys whose scores that lane holds, so P^T needs no
+  // shuffle; V^T is built from 8 rows read whole and transposed in registers
+  // (A row a of output tile jj is dim VW*a + jj).
+  auto compute = [&](int t, int stage) {
+    const uint8_t* sk = lds + stage * STAGE;
+    const uint8_t* sv = sk + KEYS * RS;
+    const int kb = t * KEYS;
+    f32x4 s[2][2];
 #pragma unroll
-    for (int js = 0; js < NSUB; ++js) {
+    for (int js = 0; js < 2; ++js) {
       s[0][js] = f32x4{0.f, 0.f, 0.f, 0.f};
       s[1][js] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < KS; ++st) {
-        const uint4 a = *(const uint4*)(lds_k + (16 * js + col) * RS + (8 * grp + 32 * st) * 2);
+        const uint4 a = *(const uint4*)(sk + (16 * js + col) * RS + (8 * grp + 32 * st) * 2);
         s[0][js] = MT::mma_16x16x32(a, qf[0][st], s[0][js]);
         s[1][js] = MT::mma_16x16x32(a, qf[1][st], s[1][js]);
       }
     }
-    const bool need_mask = kb + KEYS > mask_from;
-    uint2 pb[2][NSUB];
+    if (t >= t_mask) {  // wave-uniform: only the tiles that reach past some row's limit
+#pragma unroll
+      for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+        for (int js = 0; js < 2; ++js)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (kb + 16 * js + 4 * grp + r > lim[rg]) s[rg][js][r] = kNegInf;
+    }
+    uint4 pb[2];
 #pragma unroll
     for (int rg = 0; rg < 2; ++rg) {
-      float sv[NSUB][4];
       float mt = kNegInf;
 #pragma unroll
-      for (int js = 0; js < NSUB; ++js)
+      for (int js = 0; js < 2; ++js)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float x = s[rg][js][r] * sl2;
-          if (need_mask && kb + 16 * js + 4 * grp + r > lim[rg]) x = kNegInf;
-          sv[js][r] = x;
-          mt = fmaxf(mt, x);
-        }
+        for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[rg][js][r]);
       mt = rows4_max(mt);
-      const float m_new = fmaxf(m_run[rg], mt);
-      const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run[rg] - m_use);
-      float psum = 0.f;
-#pragma unroll
-      for (int js = 0; js < NSUB; ++js) {
-        float pr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pr[r] = fast_exp2(sv[js][r] - m_use);
-          psum += pr[r];
-        }
-        pb[rg][js] = make_uint2(MT::pack2(pr[0], pr[1]), MT::pack2(pr[2], pr[3]));
-      }
-      l_run[rg] = l_run[rg] * alpha + psum;
-      if (__builtin_amdgcn_ballot_w64(m_new > m_run[rg])) {
+      const bool grow = mt > m_run[rg] + lazy_raw;
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float alpha = grow ? fast_exp2((m_run[rg] - mt) * sl2) : 1.f;
+        if (grow) m_run[rg] = mt;
+        l_run[rg] *= alpha;
 #pragma unroll
         for (int jj = 0; jj < VW; ++jj) acc[rg][jj] *= alpha;
       }
-      m_run[rg] = m_new;
+      const float moff = m_run[rg] == kNegInf ? 0.f : -m_run[rg] * sl2;
+      float pr[2][4];
+#pragma unroll
+      for (int js = 0; js < 2; ++js)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[js][r] = fast_exp2(fmaf(s[rg][js][r], sl2, moff));
+      pb[rg] = make_uint4(MT::pack2(pr[0][0], pr[0][1]), MT::pack2(pr[0][2], pr[0][3]),
+                          MT::pack2(pr[1][0], pr[1][1]), MT::pack2(pr[1][2], pr[1][3]));
+      // row sums of the rounded probabilities the PV product uses
+      l_run[rg] = MT::sum2(pb[rg].w, MT::sum2(pb[rg].z, MT::sum2(pb[rg].y, MT::sum2(pb[rg].x, l_run[rg]))));
     }
-    // O^T += V^T P^T; lane reads rows 16js+4grp+r, elements [VW*col, VW*col+VW)
+    // V rows 4*grp+i and 16+4*grp+i, dims [VW*col, VW*col+VW), four dims
+    // (8 bytes) per read to bound the live registers
 #pragma unroll
-    for (int js = 0; js < NSUB; ++js) {
-      uint32_t vv[4][VW / 2];
+    for (int q = 0; q < VW / 4; ++q) {
+      uint32_t vv[8][2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint8_t* src = lds_v + (16 * js + 4 * grp + r) * RS + VW * col * 2;
-        if constexpr (VW == 4) {
-          const uint2 t = *(const uint2*)src;
-          vv[r][0] = t.x;
-          vv[r][1] = t.y;
-        } else {
-#pragma unroll
-          for (int i = 0; i < VW / 2; i += 4) {
-            const uint4 t = *(const uint4*)(src + 4 * i);
-            vv[r][i] = t.x;
-            vv[r][i + 1] = t.y;
-            vv[r][i + 2] = t.z;
-            vv[r][i + 3] = t.w;
-          }
-        }
+      for (int i = 0; i < 8; ++i) {
+        const uint2 q2 = *(const uint2*)(sv + (16 * (i >> 2) + 4 * grp + (i & 3)) * RS + (VW * col + 4 * q) * 2);
+        vv[i][0] = q2.x;
+        vv[i][1] = q2.y;
       }
 #pragma unroll
-      for (int jj = 0; jj < VW; ++jj) {
-        uint2 a;
-        if (jj & 1) {
-          a.x = pack_hi16(vv[0][jj >> 1], vv[1][jj >> 1]);
-          a.y = pack_hi16(vv[2][jj >> 1], vv[3][jj >> 1]);
+      for (int e = 0; e < 4; ++e) {
+        const int jj = 4 * q + e, w = e >> 1;
+        uint4 a;
+        if (e & 1) {
+          a = make_uint4(pack_hi16(vv[0][w], vv[1][w]), pack_hi16(vv[2][w], vv[3][w]),
+                         pack_hi16(vv[4][w], vv[5][w]), pack_hi16(vv[6][w], vv[7][w]));
         } else {
-          a.x = pack_lo16(vv[0][jj >> 1], vv[1][jj >> 1]);
-          a.y = pack_lo16(vv[2][jj >> 1], vv[3][jj >> 1]);
+          a = make_uint4(pack_lo16(vv[0][w], vv[1][w]), pack_lo16(vv[2][w], vv[3][w]),
+                         pack_lo16(vv[4][w], vv[5][w]), pack_lo16(vv[6][w], vv[7][w]));
         }
-        acc[0][jj] = MT::mma_16x16x16(a, pb[0][js], acc[0][jj]);
-        acc[1][jj] = MT::mma_16x16x16(a, pb[1][js], acc[1][jj]);
+        acc[0][jj] = MT::mma_16x16x32(a, pb[0], acc[0][jj]);
+        acc[1][jj] = MT::mma_16x16x32(a, pb[1], acc[1][jj]);
       }
     }
   };
 
-  if (n_kt > 0) {
-    load_tile(0);
-    store_tile();
+  // ---- page chunks (one for contexts up to kPfPageCap pages); in each, a
+  // two-stage LDS ring fed from registers loaded two tiles ahead.  Loads past
+  // the last tile repeat the last tile, so the steady loop has no conditional
+  // loads and the compiler's vmcnt waits stay exact.
+  for (c0 = 0; c0 * ps < kv_end; c0 += kPfPageCap) {
+    const int npg = min(np - c0, kPfPageCap);
     __syncthreads();
-    for (int kt = 0; kt < n_kt; ++kt) {
-      if (kt + 1 < n_kt) load_tile(kt + 1);  // global loads in flight during compute
-      compute(kt);
+    for (int i = tid; i < npg; i += THREADS) lds_pages[i] = p.kv_indices[page_base + c0 + i];
+    __syncthreads();
+    const int t0 = c0 * ps / KEYS;
+    const int t1 = min(n_kt, (c0 + kPfPageCap) * ps / KEYS);
+    const int tl = t1 - 1;
+    load_tile(t0, ra);
+    load_tile(min(t0 + 1, tl), rb);
+    store_tile(t0, ra, 0);
+    __syncthreads();
+    for (int t = t0;; t += 2) {
+      load_tile(min(t + 2, tl), ra);
+      compute(t, 0);
+      store_tile(min(t + 1, tl), rb, 1);
       __syncthreads();
-      if (kt + 1 < n_kt) {
-        store_tile();
-        __syncthreads();
-      }
+      if (t + 1 >= t1) break;
+      load_tile(min(t + 3, tl), rb);
+      compute(t + 1, 1);
+      store_tile(min(t + 2, tl), ra, 0);
+      __syncthreads();
+      if (t + 2 >= t1) break;
     }
   }
 
-  // ---- epilogue
+  // ---- epilogue: lane holds dims VW*(4*grp+r)+jj of its row
 #pragma unroll
   for (int rg = 0; rg < 2; ++rg) {
     const float l_tot = rows4_sum(l_run[rg]);
@@ -387,9 +438,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
 template <typename MT, bool FP8>
 static int launch_prefill(const PrefillParams& pp, int head_dim, int grid, hipStream_t stream) {
   switch (head_dim) {
-    case 64: hipLaunchKernelGGL((prefill_kernel<MT, FP8, 64>), dim3(grid), dim3(256), 0, stream, pp); break;
-    case 128: hipLaunchKernelGGL((prefill_kernel<MT, FP8, 128>), dim3(grid), dim3(256), 0, stream, pp); break;
-    case 256: hipLaunchKernelGGL((prefill_kernel<MT, FP8, 256>), dim3(grid), dim3(256), 0, stream, pp); break;
+    case 64: hipLaunchKernelGGL((prefill_kernel<MT, FP8, 64>), dim3(grid), dim3(64 * pf_waves(64)), 0, stream, pp); break;
+    case 128: hipLaunchKernelGGL((prefill_kernel<MT, FP8, 128>), dim3(grid), dim3(64 * pf_waves(128)), 0, stream, pp); break;
+    case 256: hipLaunchKernelGGL((prefill_kernel<MT, FP8, 256>), dim3(grid), dim3(64 * pf_waves(256)), 0, stream, pp); break;
     default: return MI_ERR_UNSUPPORTED;
   }
   return MI_OK;
@@ -404,7 +455,7 @@ extern "C" int64_t mi_prefill_workspace_bytes(int32_t batch, int32_t max_qo_toke
   using namespace mi;
   if (batch < 0 || max_qo_tokens < 0 || num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads)
     return MI_ERR_INVALID;
-  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, num_qo_heads / num_kv_heads);
+  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, num_qo_heads / num_kv_heads, head_dim);
   return L.split + split_layout(batch, num_kv_heads, head_dim, -1).total;
 }
 
@@ -423,7 +474,7 @@ extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
   if (page_size % 16 || !ok_head_dim(head_dim)) return MI_ERR_UNSUPPORTED;
   const int G = num_qo_heads / num_kv_heads;
   if (G > kShortRows) return MI_ERR_UNSUPPORTED;
-  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G);
+  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, head_dim);
   if (workspace_bytes < L.split) return MI_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
   uint8_t* ws = (uint8_t*)workspace;
@@ -431,20 +482,24 @@ extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
     hipLaunchKernelGGL(token_map_kernel, dim3((token_map_len + 255) / 256), dim3(256), 0, s, qo_indptr, kv_indptr,
                        kv_indices, last_page_len, batch, page_size, token_to_page, token_to_cache, token_map_len);
   }
-  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, qo_indptr, batch, G, L.max_tiles,
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, qo_indptr, batch, G, pf_rows(head_dim), L.max_tiles,
                      (int32_t*)(ws + L.hdr), (int2*)(ws + L.tiles));
   MI_CHECK_LAUNCH();
   return decode_plan_impl(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
                           num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, L.split, s);
 }
 
-extern "C" int mi_prefill_run(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
-                              const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
-                              const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
-                              int32_t max_qo_tokens, int32_t num_qo_heads, int32_t causal, float sm_scale,
-                              void* workspace, int64_t workspace_bytes, void* out, int64_t out_stride_token,
-                              int64_t out_stride_head, void* stream) {
-  using namespace mi;
+namespace mi {
+
+constexpr int kPhaseShort = 1;  // short-query requests: split-KV decode kernel + merge
+constexpr int kPhaseTiles = 2;  // long-query requests: MFMA prefill tiles
+
+static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                            const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                            const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                            int32_t max_qo_tokens, int32_t num_qo_heads, int32_t causal, float sm_scale,
+                            void* workspace, int64_t workspace_bytes, void* out, int64_t out_stride_token,
+                            int64_t out_stride_head, int phases, void* stream) {
   if (!kv || batch < 0 || max_qo_tokens < 0 || !workspace) return MI_ERR_INVALID;
   if (batch == 0) return MI_OK;
   if (!q || !out || !kv->data || !qo_indptr || !kv_indptr || !kv_indices || !last_page_len) return MI_ERR_INVALID;
@@ -456,14 +511,17 @@ extern "C" int mi_prefill_run(const void* q, int32_t q_dtype, int64_t q_stride_t
   if (q_dtype != MI_BF16 && q_dtype != MI_F16) return MI_ERR_UNSUPPORTED;
   if (!fp8 && kv->dtype != q_dtype) return MI_ERR_UNSUPPORTED;
   if (fp8 && (!kv->k_scale || !kv->v_scale)) return MI_ERR_INVALID;
-  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G);
+  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, D);
   if (workspace_bytes < L.split) return MI_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
-  // short-query requests: split-KV decode kernel + merge
-  int st = decode_run_impl(q, q_dtype, q_stride_token, q_stride_head, kv, qo_indptr, kv_indptr, kv_indices,
-                           last_page_len, batch, num_qo_heads, causal, sm_scale, workspace, workspace_bytes,
-                           L.split, out, out_stride_token, out_stride_head, kPhaseAttend | kPhaseMerge, s);
-  if (st != MI_OK) return st;
+  int st = MI_OK;
+  if (phases & kPhaseShort) {
+    st = decode_run_impl(q, q_dtype, q_stride_token, q_stride_head, kv, qo_indptr, kv_indptr, kv_indices,
+                         last_page_len, batch, num_qo_heads, causal, sm_scale, workspace, workspace_bytes,
+                         L.split, out, out_stride_token, out_stride_head, kPhaseAttend | kPhaseMerge, s);
+    if (st != MI_OK) return st;
+  }
+  if (!(phases & kPhaseTiles)) return MI_OK;
   // long-query requests: MFMA prefill tiles
   const uint8_t* ws = (const uint8_t*)workspace;
   PrefillParams pp;
@@ -501,3 +559,20 @@ extern "C" int mi_prefill_run(const void* q, int32_t q_dtype, int64_t q_stride_t
   MI_CHECK_LAUNCH();
   return MI_OK;
 }
+
+}  // namespace mi
+
+#define MI_PREFILL_ARGS                                                                                          \
+  const void *q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head, const mi_paged_kv *kv,          \
+      const int32_t *qo_indptr, const int32_t *kv_indptr, const int32_t *kv_indices,                             \
+      const int32_t *last_page_len, int32_t batch, int32_t max_qo_tokens, int32_t num_qo_heads, int32_t causal, \
+      float sm_scale, void *workspace, int64_t workspace_bytes, void *out, int64_t out_stride_token,             \
+      int64_t out_stride_head, void *stream
+#define MI_PREFILL_FWD(phases)                                                                                    \
+  mi::prefill_run_impl(q, q_dtype, q_stride_token, q_stride_head, kv, qo_indptr, kv_indptr, kv_indices,          \
+                       last_page_len, batch, max_qo_tokens, num_qo_heads, causal, sm_scale, workspace,           \
+                       workspace_bytes, out, out_stride_token, out_stride_head, phases, stream)
+
+extern "C" int mi_prefill_run(MI_PREFILL_ARGS) { return MI_PREFILL_FWD(mi::kPhaseShort | mi::kPhaseTiles); }
+extern "C" int mi_prefill_short(MI_PREFILL_ARGS) { return MI_PREFILL_FWD(mi::kPhaseShort); }
+extern "C" int mi_prefill_tiles(MI_PREFILL_ARGS) { return MI_PREFILL_FWD(mi::kPhaseTiles); }
