@@ -20,6 +20,7 @@ typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef i16x4 v4i16;
 typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 typedef __attribute__((ext_vector_type(2))) float f32x2;
@@ -135,6 +136,14 @@ MI_DEVICE uint32_t fp8x2_to_mt<F16>(uint32_t w, bool hi) {
 
 // ------------------------------------------------------------ lane helpers
 MI_DEVICE int lane_id() { return __lane_id(); }
+
+// gfx950 transposing LDS read (ds_read_b64_tr_b16).  In each group of 16
+// lanes, lane l receives element l%4 of the 64-bit rows addressed by lanes
+// 4k + l/4, k = 0..3 (as element k).  addr must be 8-byte aligned.
+MI_DEVICE v4i16 ds_read_tr16(const uint8_t* lds_addr) {
+  typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds_addr));
+}
 
 // Wave-uniform value in an SGPR.
 MI_DEVICE int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }

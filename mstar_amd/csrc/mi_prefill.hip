@@ -37,21 +37,27 @@ constexpr int kPfKeys = 32;                // keys per K/V tile
 constexpr int kPfPageCap = 2048;           // page ids staged in LDS at a time
 constexpr int kShortRows = 16;  // qo_len * group <= 16 -> decode kernel
 
+// Workspace: header | per-XCD queue counters | tile list | tile cost prefix | decode split plan.
+// Header words: [0] tiles, [1] units (tiles x kv-heads), [8 + x] first unit
+// of XCD x's queue (x = 0..8, [16] = units).
 struct PrefillLayout {
-  int64_t hdr, tiles, split;
+  int64_t hdr, ctr, tiles, tcum, split;
   int32_t max_tiles;
 };
+constexpr int kCtrStride = 32;  // one 128-byte line per XCD counter
 
 static PrefillLayout prefill_layout(int32_t batch, int32_t max_qo_tokens, int32_t group, int32_t head_dim) {
   const int tile_rows = pf_rows(head_dim);
   PrefillLayout L;
   const int64_t rows = (int64_t)max_qo_tokens * group;
   int64_t mt = (rows + tile_rows - 1) / tile_rows + batch;
-  if (mt > (1 << 28)) mt = 1 << 28;
+  if (mt > (1 << 21)) mt = 1 << 21;
   L.max_tiles = (int32_t)mt;
   L.hdr = 0;
-  L.tiles = 256;
-  L.split = mi_align_up(L.tiles + 8LL * L.max_tiles, 256);
+  L.ctr = 256;
+  L.tiles = L.ctr + 8 * kCtrStride * 4;
+  L.tcum = mi_align_up(L.tiles + 8LL * L.max_tiles, 256);
+  L.split = mi_align_up(L.tcum + 4LL * (L.max_tiles + 1), 256);
   return L;
 }
 
@@ -88,26 +94,81 @@ __global__ __launch_bounds__(256) void token_map_kernel(const int32_t* qo_indptr
 }
 
 // ------------------------------------------------------------ tile plan
-__global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* qo_indptr, int32_t batch,
-                                                            int32_t group, int32_t tile_rows, int32_t max_tiles,
-                                                            int32_t* hdr,
-                                                            int2* tiles) {
+// Tiles of tile_rows (token, q-head) rows, request by request, heaviest
+// (latest rows, most keys under the causal mask) first within a request.
+// A tile's cost is its number of 32-key steps.  Units (kv-head, tile) in
+// head-major order are cut into 8 contiguous runs of equal cost, one queue
+// per XCD, so each XCD's L2 serves few (request, head) KV streams and the
+// XCDs finish together.
+__device__ int pf_tile_cost(int kv_len, int qo_len, int rows_total, int row0, int tile_rows, int group,
+                            int causal) {
+  const int last_row = min(row0 + tile_rows, rows_total) - 1;
+  const int kv_end = causal ? min(kv_len, kv_len - qo_len + last_row / group + 1) : kv_len;
+  return kv_end > 0 ? (kv_end + kPfKeys - 1) / kPfKeys : 0;
+}
+
+__global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* qo_indptr, const int32_t* kv_indptr,
+                                                            const int32_t* last_page_len, int32_t batch,
+                                                            int32_t page_size, int32_t group, int32_t nkv,
+                                                            int32_t tile_rows, int32_t max_tiles, int32_t causal,
+                                                            int32_t* hdr, int2* tiles, int32_t* tcum) {
   __shared__ int smem[16];
-  int carry = 0;
+  int carry = 0, carry_cost = 0;
   for (int base = 0; base < batch; base += 1024) {
     const int b = base + (int)threadIdx.x;
-    int n = 0;
+    int n = 0, cost = 0, kv_len = 0, qo_len = 0;
     if (b < batch) {
-      const int rows = (qo_indptr[b + 1] - qo_indptr[b]) * group;
+      qo_len = qo_indptr[b + 1] - qo_indptr[b];
+      const int rows = qo_len * group;
       n = rows > kShortRows ? (rows + tile_rows - 1) / tile_rows : 0;
+      kv_len = (kv_indptr[b + 1] - kv_indptr[b] - 1) * page_size + last_page_len[b];
+      for (int i = 0; i < n; ++i)
+        cost += pf_tile_cost(kv_len, qo_len, rows, (n - 1 - i) * tile_rows, tile_rows, group, causal);
     }
-    int total;
+    int total, total_cost;
     const int first = block_exclusive_scan_1024(n, total, smem) + carry;
-    for (int i = 0; i < n && first + i < max_tiles; ++i)
-      tiles[first + i] = make_int2(b, (n - 1 - i) * tile_rows);  // causal: heaviest tile first
+    int cum = block_exclusive_scan_1024(cost, total_cost, smem) + carry_cost;
+    for (int i = 0; i < n && first + i < max_tiles; ++i) {
+      const int row0 = (n - 1 - i) * tile_rows;
+      tiles[first + i] = make_int2(b, row0);
+      tcum[first + i] = cum;
+      cum += pf_tile_cost(kv_len, qo_len, qo_len * group, row0, tile_rows, group, causal);
+    }
     carry += total;
+    carry_cost += total_cost;
   }
-  if (threadIdx.x == 0) hdr[0] = min(carry, max_tiles);
+  const int n_tiles = min(carry, max_tiles);
+  if (threadIdx.x == 0) tcum[n_tiles] = carry_cost;  // truncated lists keep a consistent prefix end
+  __syncthreads();
+  const int64_t ct = tcum[n_tiles];
+  const int64_t units = (int64_t)n_tiles * nkv;
+  const int64_t total = ct * nkv;
+  if (threadIdx.x == 0) {
+    hdr[0] = n_tiles;
+    hdr[1] = (int32_t)units;
+  }
+  if (threadIdx.x <= 8) {
+    const int x = threadIdx.x;
+    int64_t u0 = units;
+    if (x == 0) {
+      u0 = 0;
+    } else if (x < 8 && total > 0) {
+      // first unit whose cost prefix reaches ceil(x * total / 8)
+      const int64_t target = (x * total + 7) / 8;
+      int64_t lo = 0, hi = units;
+      while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        const int64_t h = mid / n_tiles, t = mid - h * n_tiles;
+        if (h * ct + tcum[t] >= target) hi = mid; else lo = mid + 1;
+      }
+      u0 = lo;
+    }
+    hdr[8 + x] = (int32_t)u0;
+  }
+}
+
+__global__ void prefill_reset_kernel(int32_t* ctr) {
+  if (threadIdx.x < 8) ctr[threadIdx.x * kCtrStride] = 0;
 }
 
 // ------------------------------------------------------------ attention
@@ -124,6 +185,7 @@ struct PrefillParams {
   const int32_t* last_page_len;
   const int32_t* hdr;
   const int2* tiles;
+  int32_t* ctr;
   void* out;
   int64_t out_stride_tok, out_stride_head;
   int32_t num_kv_heads, group, page_size, causal;
@@ -135,12 +197,16 @@ struct PrefillCfg {
   static constexpr int THREADS = 64 * pf_waves(D);
   static constexpr int ROWS = pf_rows(D);
   static constexpr int KEYS = kPfKeys;                     // keys per K/V tile
-  static constexpr int RS = D * 2 + 16;                    // LDS row stride (bytes, MFMA-type elements)
+  // LDS row strides (bytes, MFMA-type elements).  K rows step 4 banks so 16
+  // lanes reading 16 rows at one column hit distinct banks; V rows step 8
+  // banks so the 4 rows x 32 bytes of one transposing read do.
+  static constexpr int RSK = D * 2 + 16;
+  static constexpr int RSV = D * 2 + 32;
   static constexpr int ESZ = FP8 ? 1 : 2;                  // cache element size
   static constexpr int CPR = D * ESZ / 16;                 // 16-byte chunks per cached row
   static constexpr int HALF = KEYS * CPR;                  // chunks of the K (or V) half of a tile
   static constexpr int NL = (2 * HALF + THREADS - 1) / THREADS;  // loader chunks per thread
-  static constexpr int STAGE = 2 * KEYS * RS;              // one LDS stage: K rows then V rows
+  static constexpr int STAGE = KEYS * (RSK + RSV);         // one LDS stage: K rows then V rows
   static_assert(HALF % 64 == 0, "a wavefront's loader chunks must stay in one half");
   static_assert((2 * HALF) % THREADS == 0 || 2 * HALF < THREADS, "loader mapping");
 };
@@ -148,21 +214,36 @@ struct PrefillCfg {
 template <typename MT, bool FP8, int D>
 __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams p) {
   using C = PrefillCfg<MT, FP8, D>;
-  constexpr int KS = D / 32, VW = D / 16, KEYS = C::KEYS, RS = C::RS, ESZ = C::ESZ, CPR = C::CPR;
+  constexpr int KS = D / 32, VW = D / 16, KEYS = C::KEYS, RSK = C::RSK, RSV = C::RSV, ESZ = C::ESZ, CPR = C::CPR;
   constexpr int THREADS = C::THREADS, NL = C::NL, HALF = C::HALF, STAGE = C::STAGE;
   constexpr int LCH = FP8 ? 32 : 16;  // LDS bytes per loaded chunk
   constexpr float kNegInf = -__builtin_inff();
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
   __shared__ int32_t lds_pages[kPfPageCap];
 
-  // ---- XCD-aware unit: XCD x = blockIdx % 8 takes units [x*per, (x+1)*per)
+  __shared__ int s_unit;
   const int nkv = p.num_kv_heads;
   const int n_tiles = p.hdr[0];
-  const int n_units = n_tiles * nkv;
-  const int per_xcd = (n_units + 7) >> 3;
-  const int j = (int)blockIdx.x >> 3;
-  const int unit = ((int)blockIdx.x & 7) * per_xcd + j;
-  if (j >= per_xcd || unit >= n_units) return;
+  const int xcd = (int)blockIdx.x & 7;  // workgroups are dispatched to the 8 XCDs round-robin
+
+  // ---- persistent: take units from this XCD's queue, then steal from the others
+  for (;;) {
+  if (threadIdx.x == 0) {
+    int u = -1;
+    for (int k = 0; k < 8 && u < 0; ++k) {
+      const int y = (xcd + k) & 7;
+      const int first = p.hdr[8 + y], len = p.hdr[9 + y] - first;
+      if (len <= 0 || __hip_atomic_load(p.ctr + y * kCtrStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= len)
+        continue;
+      const int i = atomicAdd(p.ctr + y * kCtrStride, 1);
+      if (i < len) u = first + i;
+    }
+    s_unit = u;
+  }
+  __syncthreads();
+  const int unit = s_unit;
+  __syncthreads();
+  if (unit < 0) break;
   const int h = unit / n_tiles;
   const int tile = unit - h * n_tiles;
   const int2 te = p.tiles[tile];
@@ -232,8 +313,10 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     l_off[i] = (uint32_t)((int64_t)half * p.kv_stride * ESZ + (int64_t)(row - (row & ~15)) * tok_bytes + 16 * ch);
   }
   const int key_cap = np * ps - 16;  // last 16-row group inside the request's pages
-  uint4 ra[NL], rb[NL];
   int c0 = 0;  // first page of the page ids staged in LDS
+  // NB register buffers (even): tile t+NB is loaded while tile t is computed
+  constexpr int NB = NL <= 2 ? 4 : 2;
+  uint4 rr[NB][NL];
   auto load_tile = [&](int t, uint4 (&r)[NL]) {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -257,7 +340,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         uint4 v = r[i];
         // V rows past the KV end may hold anything (unwritten slots of the last page)
         if (l_v[i] && t * KEYS + l_row[i] >= kv_len) v = make_uint4(0, 0, 0, 0);
-        uint8_t* dst = lds + stage * STAGE + half * KEYS * RS + row * RS + LCH * ch;
+        uint8_t* dst = lds + stage * STAGE + (half ? KEYS * RSK + row * RSV : row * RSK) + LCH * ch;
         if constexpr (FP8) {  // 16 fp8 -> 16 MFMA-type elements (32 bytes)
           const uint32_t w[4] = {v.x, v.y, v.z, v.w};
           uint32_t o[8];
@@ -296,11 +379,10 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // O^T += V^T.P^T as one 16x16x32 MFMA per 16 output dims.  The MFMA k
   // index i of lane group grp stands for key 4*grp+i (i < 4) or 16+4*grp+i-4
   // (i >= 4): exactly the keys whose scores that lane holds, so P^T needs no
-  // shuffle; V^T is built from 8 rows read whole and transposed in registers
-  // (A row a of output tile jj is dim VW*a + jj).
+  // shuffle.
   auto compute = [&](int t, int stage) {
     const uint8_t* sk = lds + stage * STAGE;
-    const uint8_t* sv = sk + KEYS * RS;
+    const uint8_t* vt0 = sk + KEYS * RSK + (4 * grp + ((lane & 15) >> 2)) * RSV + 8 * (lane & 3);
     const int kb = t * KEYS;
     f32x4 s[2][2];
 #pragma unroll
@@ -309,7 +391,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       s[1][js] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < KS; ++st) {
-        const uint4 a = *(const uint4*)(sk + (16 * js + col) * RS + (8 * grp + 32 * st) * 2);
+        const uint4 a = *(const uint4*)(sk + (16 * js + col) * RSK + (8 * grp + 32 * st) * 2);
         s[0][js] = MT::mma_16x16x32(a, qf[0][st], s[0][js]);
         s[1][js] = MT::mma_16x16x32(a, qf[1][st], s[1][js]);
       }
@@ -351,38 +433,25 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       // row sums of the rounded probabilities the PV product uses
       l_run[rg] = MT::sum2(pb[rg].w, MT::sum2(pb[rg].z, MT::sum2(pb[rg].y, MT::sum2(pb[rg].x, l_run[rg]))));
     }
-    // V rows 4*grp+i and 16+4*grp+i, dims [VW*col, VW*col+VW), four dims
-    // (8 bytes) per read to bound the live registers
+    // V^T fragments with the transposing LDS read: in each 16-lane group,
+    // lane j addresses row 4*grp + j/4 (+16 for MFMA k-slots 4..7) at dims
+    // 16*jj + 4*(j%4) .. +3, and lane l receives the group's 4 keys at dim
+    // 16*jj + l%16 -- the A operand of output tile jj (A row a = dim 16*jj + a).
 #pragma unroll
-    for (int q = 0; q < VW / 4; ++q) {
-      uint32_t vv[8][2];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint2 q2 = *(const uint2*)(sv + (16 * (i >> 2) + 4 * grp + (i & 3)) * RS + (VW * col + 4 * q) * 2);
-        vv[i][0] = q2.x;
-        vv[i][1] = q2.y;
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int jj = 4 * q + e, w = e >> 1;
-        uint4 a;
-        if (e & 1) {
-          a = make_uint4(pack_hi16(vv[0][w], vv[1][w]), pack_hi16(vv[2][w], vv[3][w]),
-                         pack_hi16(vv[4][w], vv[5][w]), pack_hi16(vv[6][w], vv[7][w]));
-        } else {
-          a = make_uint4(pack_lo16(vv[0][w], vv[1][w]), pack_lo16(vv[2][w], vv[3][w]),
-                         pack_lo16(vv[4][w], vv[5][w]), pack_lo16(vv[6][w], vv[7][w]));
-        }
-        acc[0][jj] = MT::mma_16x16x32(a, pb[0], acc[0][jj]);
-        acc[1][jj] = MT::mma_16x16x32(a, pb[1], acc[1][jj]);
-      }
+    for (int jj = 0; jj < VW; ++jj) {
+      const v4i16 x0 = ds_read_tr16(vt0 + 32 * jj);
+      const v4i16 x1 = ds_read_tr16(vt0 + 16 * RSV + 32 * jj);
+      const uint2 a0 = bitcast<uint2>(x0), a1 = bitcast<uint2>(x1);
+      const uint4 a = make_uint4(a0.x, a0.y, a1.x, a1.y);
+      acc[0][jj] = MT::mma_16x16x32(a, pb[0], acc[0][jj]);
+      acc[1][jj] = MT::mma_16x16x32(a, pb[1], acc[1][jj]);
     }
   };
 
   // ---- page chunks (one for contexts up to kPfPageCap pages); in each, a
-  // two-stage LDS ring fed from registers loaded two tiles ahead.  Loads past
-  // the last tile repeat the last tile, so the steady loop has no conditional
-  // loads and the compiler's vmcnt waits stay exact.
+  // two-stage LDS ring fed from NB register buffers (loads run NB tiles
+  // ahead).  Loads past the last tile repeat the last tile, so the steady
+  // loop has no conditional loads and the compiler's vmcnt waits stay exact.
   for (c0 = 0; c0 * ps < kv_end; c0 += kPfPageCap) {
     const int npg = min(np - c0, kPfPageCap);
     __syncthreads();
@@ -391,25 +460,28 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     const int t0 = c0 * ps / KEYS;
     const int t1 = min(n_kt, (c0 + kPfPageCap) * ps / KEYS);
     const int tl = t1 - 1;
-    load_tile(t0, ra);
-    load_tile(min(t0 + 1, tl), rb);
-    store_tile(t0, ra, 0);
+    // prologue: tiles t0 .. t0+NB-1 in flight, tile t0 in LDS stage 0
+#pragma unroll
+    for (int u = 0; u < NB; ++u) load_tile(min(t0 + u, tl), rr[u]);
+    store_tile(t0, rr[0], 0);
     __syncthreads();
-    for (int t = t0;; t += 2) {
-      load_tile(min(t + 2, tl), ra);
-      compute(t, 0);
-      store_tile(min(t + 1, tl), rb, 1);
-      __syncthreads();
-      if (t + 1 >= t1) break;
-      load_tile(min(t + 3, tl), rb);
-      compute(t + 1, 1);
-      store_tile(min(t + 2, tl), ra, 0);
-      __syncthreads();
-      if (t + 2 >= t1) break;
+    bool done = false;
+    for (int t = t0; !done; t += NB) {
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        load_tile(min(t + u + NB, tl), rr[u]);  // rr[u] held tile t+u, stored last step
+        compute(t + u, u & 1);
+        store_tile(min(t + u + 1, tl), rr[(u + 1) % NB], (u + 1) & 1);
+        __syncthreads();
+        if (t + u + 1 >= t1) {
+          done = true;
+          break;
+        }
+      }
     }
   }
 
-  // ---- epilogue: lane holds dims VW*(4*grp+r)+jj of its row
+  // ---- epilogue: lane holds dims 16*jj + 4*grp + r of its row
 #pragma unroll
   for (int rg = 0; rg < 2; ++rg) {
     const float l_tot = rows4_sum(l_run[rg]);
@@ -420,19 +492,12 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     uint16_t* orow = (uint16_t*)p.out + (int64_t)(qo_start + tok) * p.out_stride_tok +
                      (int64_t)(h * G + g) * p.out_stride_head;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      uint32_t w[VW / 2];
-#pragma unroll
-      for (int i = 0; i < VW / 2; ++i) w[i] = MT::pack2(acc[rg][2 * i][r] * inv, acc[rg][2 * i + 1][r] * inv);
-      uint16_t* dst = orow + VW * (4 * grp + r);
-      if constexpr (VW == 4) {
-        *(uint2*)dst = make_uint2(w[0], w[1]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
-      }
+    for (int jj = 0; jj < VW; ++jj) {
+      const f32x4 o = acc[rg][jj];
+      *(uint2*)(orow + 16 * jj + 4 * grp) = make_uint2(MT::pack2(o[0] * inv, o[1] * inv), MT::pack2(o[2] * inv, o[3] * inv));
     }
   }
+  }  // unit loop
 }
 
 template <typename MT, bool FP8>
@@ -482,8 +547,10 @@ extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
     hipLaunchKernelGGL(token_map_kernel, dim3((token_map_len + 255) / 256), dim3(256), 0, s, qo_indptr, kv_indptr,
                        kv_indices, last_page_len, batch, page_size, token_to_page, token_to_cache, token_map_len);
   }
-  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, qo_indptr, batch, G, pf_rows(head_dim), L.max_tiles,
-                     (int32_t*)(ws + L.hdr), (int2*)(ws + L.tiles));
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, qo_indptr, kv_indptr, last_page_len, batch,
+                     page_size, G, num_kv_heads, pf_rows(head_dim), L.max_tiles, /*cost model: causal*/ 1,
+                     (int32_t*)(ws + L.hdr),
+                     (int2*)(ws + L.tiles), (int32_t*)(ws + L.tcum));
   MI_CHECK_LAUNCH();
   return decode_plan_impl(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
                           num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, L.split, s);
@@ -541,6 +608,7 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
   pp.last_page_len = last_page_len;
   pp.hdr = (const int32_t*)(ws + L.hdr);
   pp.tiles = (const int2*)(ws + L.tiles);
+  pp.ctr = (int32_t*)((uint8_t*)workspace + L.ctr);
   pp.out = out;
   pp.out_stride_tok = out_stride_token;
   pp.out_stride_head = out_stride_head;
@@ -549,8 +617,14 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
   pp.page_size = kv->page_size;
   pp.causal = causal ? 1 : 0;
   pp.scale_log2 = sm_scale * 1.4426950408889634f;
+  // persistent grid: one workgroup per CU (each holds two wavefronts per SIMD),
+  // never more than there are units
+  int dev = 0, ncu = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return MI_ERR_LAUNCH;
   const int64_t units = (int64_t)L.max_tiles * nkv;
-  const int grid = (int)((units + 7) / 8 * 8);
+  const int grid = (int)(((units < ncu ? units : (int64_t)ncu) + 7) / 8 * 8);
+  hipLaunchKernelGGL(prefill_reset_kernel, dim3(1), dim3(64), 0, s, pp.ctr);
   if (q_dtype == MI_BF16)
     st = fp8 ? launch_prefill<BF16, true>(pp, D, grid, s) : launch_prefill<BF16, false>(pp, D, grid, s);
   else
