@@ -323,6 +323,7 @@ class PagedPrefillWrapper:
         self.causal = True
         self._workspace = workspace_buffer
         self._staging = _Staging()
+        self._side: torch.cuda.Stream | None = None
         self._n_req = 0
         if use_cuda_graph:
             assert batch_size is not None, "batch_size required for CUDA graph mode"
@@ -435,15 +436,23 @@ class PagedPrefillWrapper:
         qs = _q_strides(q, "q")
         os_ = _q_strides(out, "out")
         ws_bytes = self._workspace.numel() * self._workspace.element_size()
-        _lib.check(
-            _lib.lib().mi_prefill_run(
-                q.data_ptr(), _lib.TORCH_TO_MI[q.dtype], qs[0], qs[1], desc, self._qo.data_ptr(),
+        args = [q.data_ptr(), _lib.TORCH_TO_MI[q.dtype], qs[0], qs[1], desc, self._qo.data_ptr(),
                 self._indptr.data_ptr(), self._indices.data_ptr(), self._last.data_ptr(), self._plan_batch,
                 self._plan_max_tokens, self.num_qo_heads, 1 if self.causal else 0, 1.0 / math.sqrt(self.head_dim),
-                self._workspace.data_ptr(), ws_bytes, out.data_ptr(), os_[0], os_[1], _lib.stream_ptr(q.device),
-            ),
-            "mi_prefill_run",
-        )
+                self._workspace.data_ptr(), ws_bytes, out.data_ptr(), os_[0], os_[1], None]
+        # The MFMA tiles (long-query requests) and the split-KV decode of the
+        # short-query requests write disjoint rows: run the HBM-bound decode
+        # on a side stream so it overlaps the compute-bound tiles.
+        main = torch.cuda.current_stream(q.device)
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=q.device)
+        side = self._side
+        side.wait_stream(main)
+        args[-1] = main.cuda_stream
+        _lib.check(_lib.lib().mi_prefill_tiles(*args), "mi_prefill_tiles")
+        args[-1] = side.cuda_stream
+        _lib.check(_lib.lib().mi_prefill_short(*args), "mi_prefill_short")
+        main.wait_stream(side)
         return out
 
     def set_kv_cache(self, kv_cache_layer: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
