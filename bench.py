@@ -334,10 +334,46 @@ def bench_decode(args, dev) -> dict:
             "algorithmic_bytes": int(np.mean(bytes_per)),
         },
     }
+    res["rope"] = bench_rope(q, k, np.array([cm._get_state(r).seq_len for r in rids]), args.steps)
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
         res["cpu_baseline"] = cpu_baseline(bt, kv, q, k, v, cm.kv_scales)
     return res
+
+
+def bench_rope(q, k, positions: np.ndarray, steps: int, per_graph: int = 20) -> dict:
+    """apply_rope on this step's q and k (in place, on copies): HBM read + write of both.
+
+    The kernel is shorter than a Python launch, so launches are captured in a
+    HIP graph and replayed; the per-launch time is the replay time / launches.
+    """
+    from mstar_amd.rope import apply_rope_pos_ids_inplace
+
+    qc, kc = q.clone(), k.clone()
+    pos = torch.as_tensor(positions, dtype=torch.int64, device=q.device)
+    side = torch.cuda.Stream(device=q.device)
+    side.wait_stream(torch.cuda.current_stream(q.device))
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            apply_rope_pos_ids_inplace(qc, kc, pos, rope_theta=1e6)
+    torch.cuda.current_stream(q.device).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(per_graph):
+            apply_rope_pos_ids_inplace(qc, kc, pos, rope_theta=1e6)
+    graph.replay()
+    torch.cuda.synchronize()
+    evs = _kernel_events(max(steps // 5, 3), 2)
+    for e0, e1 in evs:
+        e0.record()
+        graph.replay()
+        e1.record()
+    torch.cuda.synchronize()
+    us = float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3 / per_graph
+    nbytes = 2 * (qc.numel() + kc.numel()) * qc.element_size() + pos.numel() * 8
+    return {"kernel": "rope_kernel", "what": "apply_rope_pos_ids_inplace on the step's q [B, Hq, D] and k [B, Hkv, D], "
+            f"{per_graph} launches per HIP graph replay", "kernel_us": us, "algorithmic_bytes": nbytes,
+            "GBps": nbytes / (us * 1e-6) / 1e9}
 
 
 def prefill_flops(bt) -> tuple[int, int]:

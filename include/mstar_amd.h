@@ -30,6 +30,8 @@ extern "C" {
 #define MI_F16 1
 #define MI_F32 2
 #define MI_FP8_E4M3 3 /* OCP e4m3fn (gfx950 native), max 448, per-head fp32 scales */
+#define MI_I32 4       /* index / position dtypes */
+#define MI_I64 5
 
 /* status codes */
 #define MI_OK 0
@@ -217,6 +219,32 @@ int mi_prefill_tiles(const void* q, int32_t q_dtype, int64_t q_stride_token, int
                      int32_t max_qo_tokens, int32_t num_qo_heads, int32_t causal, float sm_scale,
                      void* workspace, int64_t workspace_bytes, void* out, int64_t out_stride_token,
                      int64_t out_stride_head, void* stream);
+
+/* ------------------------------------------------------------------------
+ * RoPE on the packed batch (the path's next row: the rotation every layer
+ * applies to q and k right before the append and the attention).
+ * mi_rope_positions replaces the position list of
+ * BatchedCacheManager._plan_rope_impl (mstar/engine/cache_manager.py:480-492):
+ *   pos_ids[t] = position_id_start[r] + (t - qo_indptr[r]),  t < num_tokens.
+ * mi_rope_apply replaces the FlashInfer call of BatchedCacheManager.apply_rope
+ * (cache_manager.py:702-760; flashinfer.rope.apply_rope_pos_ids_inplace and
+ * apply_llama31_rope_pos_ids_inplace): q [num_tokens, num_qo_heads, head_dim]
+ * and k [num_tokens, num_kv_heads, head_dim] (bf16 or f16, element strides,
+ * head_dim contiguous) are rotated in place.  Dims [0, rotary_dim) turn in
+ * pairs (i, i + rotary_dim/2), or (2i, 2i+1) when interleave != 0, by the
+ * fp32 angle pos * f_i, f_i = theta^(-2i/rotary_dim) / rope_scale; with
+ * llama31 != 0 the frequency is blended towards theta^(-2i/rotary_dim) by
+ * clamp(old_context_len * g / (2 pi (high - low)) - low / (high - low), 0, 1).
+ * rotary_dim and head_dim must be multiples of 8; pos_dtype MI_I32 or MI_I64.
+ * ------------------------------------------------------------------------ */
+int mi_rope_positions(const int32_t* qo_indptr, const int32_t* position_id_start, int32_t batch,
+                      int64_t* pos_ids, int32_t num_tokens, void* stream);
+int mi_rope_apply(void* q, int64_t q_stride_token, int64_t q_stride_head, int32_t num_qo_heads, void* k,
+                  int64_t k_stride_token, int64_t k_stride_head, int32_t num_kv_heads, int32_t dtype,
+                  int32_t head_dim, int32_t rotary_dim, const void* pos_ids, int32_t pos_dtype,
+                  int32_t num_tokens, int32_t interleave, float rope_scale, float rope_theta,
+                  int32_t llama31, float low_freq_factor, float high_freq_factor, float old_context_len,
+                  void* stream);
 
 #ifdef __cplusplus
 }

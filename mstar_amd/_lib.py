@@ -24,6 +24,8 @@ MI_BF16 = 0
 MI_F16 = 1
 MI_F32 = 2
 MI_FP8_E4M3 = 3
+MI_I32 = 4
+MI_I64 = 5
 
 MI_OK = 0
 
@@ -105,6 +107,12 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _I32, _I64, _I64, ctypes.POINTER(MiPagedKV), _P, _P, _P, _P, _I32, _I32, _I32, _I32, _F32,
          _P, _I64, _P, _I64, _I64, _P],
+    ),
+    "mi_rope_positions": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _P]),
+    "mi_rope_apply": (
+        ctypes.c_int,
+        [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _I32, _I32, _I32, _F32, _F32,
+         _I32, _F32, _F32, _F32, _P],
     ),
 }
 

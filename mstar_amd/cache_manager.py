@@ -2,7 +2,7 @@
 
 Keeps the methods M*'s model code calls on ``mstar.engine.cache_manager.
 BatchedCacheManager`` (``cache_manager.py:56-881``): ``plan_attention``,
-``run_attention``, ``set_layer_idx``, ``set_active_label(s)``,
+``run_attention``, ``plan_rope``, ``apply_rope``, ``set_layer_idx``, ``set_active_label(s)``,
 ``get_qo_indptr_buf``, ``advance_seq_len(s)``, ``set_custom_pos_advance``,
 ``flush_to_store``, plus the pre-planned-label fast path used by the CUDA-graph
 runner (``_pre_planned_labels``, ``cache_manager.py:202-217``).
@@ -28,6 +28,9 @@ import torch
 from . import _lib
 from .kv_store import KVCacheConfig, KVRequestState, PagedAllocationManager
 from .paged_attention import PagedDecodeWrapper, PagedPrefillWrapper
+from .rope import apply_llama31_rope_pos_ids_inplace, apply_rope_pos_ids_inplace, rope_positions
+
+_LLAMA31_KEYS = ("low_freq_factor", "high_freq_factor", "old_context_len")
 
 
 @dataclass
@@ -260,6 +263,76 @@ class BatchedCacheManager:
             for rid in self.request_ids:
                 self.alloc_manager.flush_to_store(rid, label=label, layers=layer_idx)
         return ps.wrapper.run(q, layer, ks, vs).to(orig_dtype)
+
+    # ------------------------------------------------------------ rope
+    def plan_rope(self, seq_lens: list[int], pos_ids: torch.Tensor | None = None, label: str | None = None) -> None:
+        """Position ids for ``apply_rope`` (``cache_manager.py:426-520``).
+
+        Without ``pos_ids``, request r contributes ``position_id_start[r] ..
+        + seq_lens[r] - 1``; the list is expanded on the GPU from one small
+        upload (cumulative lengths + starts) instead of a Python list of every
+        token.  In CUDA-graph mode an existing ``pos_ids`` buffer is rewritten
+        in place so captured launches keep their address.
+        """
+        eff = label if label is not None else self._single_active_label()
+        ps = self._plan_states.get(eff)
+        if ps is None:
+            ps = self._plan_states[eff] = _PlanState()
+        if pos_ids is not None:
+            src = pos_ids.to(device=self.device, dtype=torch.long)
+            if self._cuda_graph_mode and ps.pos_ids is not None:
+                ps.pos_ids[: src.shape[0]].copy_(src, non_blocking=True)
+            else:
+                ps.pos_ids = src
+            return
+        b = len(self.request_ids)
+        if len(seq_lens) != b:
+            raise ValueError(f"{len(seq_lens)} seq_lens for {b} requests")
+        meta = np.empty(2 * b + 1, dtype=np.int32)
+        meta[0] = 0
+        meta[1:b + 1] = np.cumsum(seq_lens, dtype=np.int64)
+        meta[b + 1:] = [self._get_state(rid, eff).position_id_start for rid in self.request_ids]
+        n = int(meta[b]) if b else 0
+        if self._cuda_graph_mode and ps.pos_ids is not None:
+            if ps.pos_ids.shape[0] < n:
+                raise ValueError(f"{n} positions do not fit the static pos_ids buffer ({ps.pos_ids.shape[0]})")
+            out = ps.pos_ids
+        else:
+            out = torch.empty(n, dtype=torch.long, device=self.device)
+        if n:
+            dev = self._pack.upload(meta)
+            rope_positions(dev[: b + 1], dev[b + 1:], out, n)
+        ps.pos_ids = out
+
+    def apply_rope(self, q: torch.Tensor, k: torch.Tensor, rotary_dim: int | None = None, interleave: bool = False,
+                   rope_scale: float = 1, rope_theta: float = 10000.0, rope_dtype=None, **kwargs):
+        """RoPE at the active label's planned positions (``cache_manager.py:702-760``).
+
+        Same dtype handling as the reference: ``rope_dtype`` if given, else the
+        autocast dtype, else fp32 inputs run in bf16; q and k are rotated in
+        place in that dtype and returned in the caller's dtype.  Llama-3.1
+        smoothing applies when any of ``low_freq_factor``,
+        ``high_freq_factor``, ``old_context_len`` is passed (not None).
+        """
+        label = self._single_active_label()
+        ps = self._plan_states[label]
+        assert ps.pos_ids is not None, "plan_rope() must run before apply_rope()"
+        orig_dtype = q.dtype
+        if rope_dtype is not None:
+            q, k = q.to(rope_dtype), k.to(rope_dtype)
+        elif torch.is_autocast_enabled("cuda"):
+            dt = torch.get_autocast_dtype("cuda")
+            q, k = q.to(dt), k.to(dt)
+        elif q.dtype == torch.float32:
+            q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+        llama31 = {key: v for key, v in kwargs.items() if key in _LLAMA31_KEYS and v is not None}
+        if llama31:
+            apply_llama31_rope_pos_ids_inplace(q, k, ps.pos_ids, rotary_dim=rotary_dim, interleave=interleave,
+                                               rope_scale=rope_scale, rope_theta=rope_theta, **llama31)
+        else:
+            apply_rope_pos_ids_inplace(q, k, ps.pos_ids, rotary_dim=rotary_dim, interleave=interleave,
+                                       rope_scale=rope_scale, rope_theta=rope_theta)
+        return q.to(orig_dtype), k.to(orig_dtype)
 
     # ------------------------------------------------------------ advance
     def advance_seq_len(self, n: int | None = None, pos_id_n: int | None = None) -> None:

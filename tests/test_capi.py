@@ -89,3 +89,22 @@ def test_unsupported_shapes_are_reported(L):
     assert L.mi_decode_plan(p, p, p, p, 1, 8, 32, 4, 128, None, p, 1 << 30, None) == MI_ERR_UNSUPPORTED
     assert L.mi_decode_plan(p, p, p, p, 1, 16, 32, 4, 96, None, p, 1 << 30, None) == MI_ERR_UNSUPPORTED
 
+
+
+def test_rope_arguments_are_checked(L):
+    buf = (ctypes.c_int32 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    # rotary_dim not a multiple of 8, rotary_dim > head_dim, fp32 tensors, zero rope_scale
+    assert L.mi_rope_apply(p, 128, 128, 1, p, 128, 128, 1, 0, 128, 12, p, 4, 1, 0, 1.0, 1e4, 0, 1.0, 4.0, 8192.0,
+                           None) == MI_ERR_UNSUPPORTED
+    assert L.mi_rope_apply(p, 128, 128, 1, p, 128, 128, 1, 0, 64, 128, p, 4, 1, 0, 1.0, 1e4, 0, 1.0, 4.0, 8192.0,
+                           None) == MI_ERR_UNSUPPORTED
+    assert L.mi_rope_apply(p, 128, 128, 1, p, 128, 128, 1, 2, 128, 128, p, 4, 1, 0, 1.0, 1e4, 0, 1.0, 4.0, 8192.0,
+                           None) == MI_ERR_UNSUPPORTED
+    assert L.mi_rope_apply(p, 128, 128, 1, p, 128, 128, 1, 0, 128, 128, p, 4, 1, 0, 0.0, 1e4, 0, 1.0, 4.0, 8192.0,
+                           None) == MI_ERR_INVALID
+    # llama31 needs high > low > 0
+    assert L.mi_rope_apply(p, 128, 128, 1, p, 128, 128, 1, 0, 128, 128, p, 4, 1, 0, 8.0, 5e5, 1, 4.0, 1.0, 8192.0,
+                           None) == MI_ERR_INVALID
+    assert L.mi_rope_positions(None, None, 0, None, 5, None) == MI_ERR_INVALID
+    assert L.mi_rope_positions(None, None, 0, None, 0, None) == 0
