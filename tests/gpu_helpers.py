@@ -10,6 +10,7 @@ import torch
 from mstar_amd import synthetic as S
 from oracle import attention as A
 from oracle import packing as P
+from oracle import rope as R
 
 
 def log(msg: str) -> None:
@@ -51,4 +52,31 @@ def decode_reference(q, cache_cpu, kv_indptr, kv_indices, last, k_scale=None, v_
                              k_scale=k_scale, v_scale=v_scale)
 
 
-__all__ = ["S", "A", "P", "log", "random_cache", "custom_batch", "workspace", "max_abs", "decode_reference"]
+# RoPE tolerance: output rounding of both sides plus one fp32 ulp of the
+# frequency at the token's position (pos * f * 2^-23 rad, doubled for margin)
+# times the pair magnitude.
+ROPE_REL = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -10}
+
+
+def rope_bound(x, ref, pos, rd, interleave, scale, theta, llama31):
+    """Per-element tolerance (see module docstring)."""
+    half = rd // 2
+    f = R.frequencies(rd, scale, theta, llama31).double()
+    ang_err = torch.as_tensor(np.asarray(pos, dtype=np.float64))[:, None] * f[None, :] * 2.0 ** -21  # [T, half]
+    xf = x.double()
+    if interleave:
+        mag = torch.sqrt(xf[..., 0:rd:2] ** 2 + xf[..., 1:rd:2] ** 2)
+    else:
+        mag = torch.sqrt(xf[..., :half] ** 2 + xf[..., half:rd] ** 2)
+    pair = mag * ang_err[:, None, :]
+    b = ROPE_REL[x.dtype] * ref.double().abs() + 1e-6
+    if interleave:
+        b[..., 0:rd:2] += pair
+        b[..., 1:rd:2] += pair
+    else:
+        b[..., :half] += pair
+        b[..., half:rd] += pair
+    return b
+
+
+__all__ = ["S", "A", "P", "log", "random_cache", "custom_batch", "workspace", "max_abs", "decode_reference", "rope_bound"]

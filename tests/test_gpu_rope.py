@@ -11,39 +11,17 @@ import numpy as np
 import pytest
 import torch
 
+from gpu_helpers import rope_bound
 from oracle import rope as R
 
 pytestmark = pytest.mark.gpu
-
-REL = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -10}
-
-
-def _bound(x, ref, pos, rd, interleave, scale, theta, llama31, dtype):
-    """Per-element tolerance (see module docstring)."""
-    half = rd // 2
-    f = R.frequencies(rd, scale, theta, llama31).double()
-    ang_err = torch.as_tensor(np.asarray(pos, dtype=np.float64))[:, None] * f[None, :] * 2.0 ** -21  # [T, half]
-    xf = x.double()
-    if interleave:
-        mag = torch.sqrt(xf[..., 0:rd:2] ** 2 + xf[..., 1:rd:2] ** 2)
-    else:
-        mag = torch.sqrt(xf[..., :half] ** 2 + xf[..., half:rd] ** 2)
-    pair = mag * ang_err[:, None, :]
-    b = REL[dtype] * ref.double().abs() + 1e-6
-    if interleave:
-        b[..., 0:rd:2] += pair
-        b[..., 1:rd:2] += pair
-    else:
-        b[..., :half] += pair
-        b[..., half:rd] += pair
-    return b
 
 
 def _check(x_in, x_out, pos, rd, interleave, scale, theta, llama31):
     ref = R.rope(x_in.cpu(), pos, rotary_dim=rd, interleave=interleave, rope_scale=scale, rope_theta=theta,
                  llama31=llama31)
     got = x_out.cpu().double()
-    bound = _bound(x_in.cpu(), ref, pos, rd, interleave, scale, theta, llama31, x_in.dtype)
+    bound = rope_bound(x_in.cpu(), ref, pos, rd, interleave, scale, theta, llama31)
     err = (got - ref.double()).abs()
     assert (err <= bound).all(), f"max err {err.max().item():.3e}, worst ratio {(err / bound).max().item():.2f}"
     assert torch.equal(x_out[..., rd:].cpu(), x_in[..., rd:].cpu())
