@@ -246,6 +246,19 @@ int mi_rope_apply(void* q, int64_t q_stride_token, int64_t q_stride_head, int32_
                   int32_t llama31, float low_freq_factor, float high_freq_factor, float old_context_len,
                   void* stream);
 
+/* ------------------------------------------------------------------------
+ * Page snapshot copies (the path's next row: multi-label / CFG planning).
+ * mi_copy_pages replaces the per-page copies of BatchedCacheManager.snapshot_all
+ * (mstar/engine/cache_manager.py:840-870): for i < num_pairs and every layer l,
+ *   page dst_pages[i] of layer l := page src_pages[i] of layer l
+ * in a pool laid out as [num_layers][max_pages][page_bytes...] with the given
+ * byte strides (16-byte aligned).  No destination may also be a source in
+ * the same call.  Pairs with ids outside [0, max_pages) are skipped.
+ * ------------------------------------------------------------------------ */
+int mi_copy_pages(void* pool, int64_t layer_stride_bytes, int32_t num_layers, int64_t page_stride_bytes,
+                  int64_t page_bytes, int64_t max_pages, const int32_t* src_pages, const int32_t* dst_pages,
+                  int32_t num_pairs, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

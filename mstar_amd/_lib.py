@@ -109,6 +109,7 @@ SIGNATURES = {
          _P, _I64, _P, _I64, _I64, _P],
     ),
     "mi_rope_positions": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _P]),
+    "mi_copy_pages": (ctypes.c_int, [_P, _I64, _I32, _I64, _I64, _I64, _P, _P, _I32, _P]),
     "mi_rope_apply": (
         ctypes.c_int,
         [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _I32, _I32, _I32, _F32, _F32,

@@ -2,7 +2,8 @@
 
 Keeps the methods M*'s model code calls on ``mstar.engine.cache_manager.
 BatchedCacheManager`` (``cache_manager.py:56-881``): ``plan_attention``,
-``run_attention``, ``plan_rope``, ``apply_rope``, ``set_layer_idx``, ``set_active_label(s)``,
+``run_attention``, ``plan_rope``, ``apply_rope``, ``plan_attention_batched_cfg``,
+``plan_rope_batched_cfg``, ``snapshot_all``, ``set_layer_idx``, ``set_active_label(s)``,
 ``get_qo_indptr_buf``, ``advance_seq_len(s)``, ``set_custom_pos_advance``,
 ``flush_to_store``, plus the pre-planned-label fast path used by the CUDA-graph
 runner (``_pre_planned_labels``, ``cache_manager.py:202-217``).
@@ -161,20 +162,17 @@ class BatchedCacheManager:
             return
         self._plan_attention_impl(seq_lens, dtype, is_causal, write_store, effective)
 
-    def _plan_attention_impl(self, seq_lens, dtype, is_causal, write_store, label) -> None:
-        assert self.kv_cache is not None
-        if dtype is None:
-            dtype = torch.bfloat16 if self.kv_cache.dtype == torch.float8_e4m3fn else self.kv_cache.dtype
-        cfg = self.kv_cache_config
-        ps_ = cfg.page_size
-        b = len(self.request_ids)
-        if len(seq_lens) != b:
-            raise ValueError(f"{len(seq_lens)} seq_lens for {b} requests")
-        # host: FIFO allocation in batch order (cache_manager.py:278-285); raises
-        # AllocationFailedError before any kernel is launched.
+    def _alloc_entries(self, entries: list[tuple[str, str]], seq_lens) -> np.ndarray:
+        """FIFO allocation in batch order (``cache_manager.py:278-285``) and the pack
+        kernel's per-entry meta ``[slot | seq_len | new_len | num_pages]``.
+
+        Raises AllocationFailedError before any kernel is launched."""
+        n = len(entries)
+        if len(seq_lens) != n:
+            raise ValueError(f"{len(seq_lens)} seq_lens for {n} requests")
         states = []
-        meta = np.empty((4, b), dtype=np.int32)
-        for i, rid in enumerate(self.request_ids):
+        meta = np.empty((4, n), dtype=np.int32)
+        for i, (rid, label) in enumerate(entries):
             st = self._get_state(rid, label)
             sl = int(seq_lens[i])
             self.alloc_manager.alloc(rid, label=label, seq_len=st.seq_len + sl)
@@ -182,9 +180,34 @@ class BatchedCacheManager:
             meta[1, i] = st.seq_len
             meta[2, i] = sl
             meta[3, i] = len(st.page_indices)
-        bt = self.alloc_manager.block_table
-        bt.sync(states)
+        self.alloc_manager.block_table.sync(states)
         meta[0] = [st.slot for st in states]
+        return meta
+
+    def _launch_pack(self, meta: np.ndarray, qo, kv_indptr, kv_indices, last, loc) -> None:
+        b = meta.shape[1]
+        total_pages = int(meta[3].sum())
+        dmeta = self._pack.upload(meta.reshape(-1))
+        bt = self.alloc_manager.block_table
+        grid = max(1, min(64, (total_pages + 8191) // 8192))
+        base = dmeta.data_ptr()
+        _lib.check(
+            _lib.lib().mi_pack(
+                base, base + 4 * b, base + 8 * b, base + 12 * b, b, bt.table.data_ptr(), bt.stride,
+                self.kv_cache_config.page_size, qo.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
+                last.data_ptr(), loc.data_ptr() if loc is not None else None, grid, _lib.stream_ptr(self.device),
+            ),
+            "mi_pack",
+        )
+
+    def _plan_attention_impl(self, seq_lens, dtype, is_causal, write_store, label) -> None:
+        assert self.kv_cache is not None
+        if dtype is None:
+            dtype = torch.bfloat16 if self.kv_cache.dtype == torch.float8_e4m3fn else self.kv_cache.dtype
+        cfg = self.kv_cache_config
+        ps_ = cfg.page_size
+        b = len(self.request_ids)
+        meta = self._alloc_entries([(rid, label) for rid in self.request_ids], seq_lens)
         total_pages = int(meta[3].sum())
         is_decode = all(int(s) == 1 for s in seq_lens)
 
@@ -206,7 +229,6 @@ class BatchedCacheManager:
             self._plan_states[label] = ps
 
         # device: one upload of [slot | seq_len | new_len | num_pages], one pack kernel
-        dmeta = self._pack.upload(meta.reshape(-1))
         graph_static = isinstance(wrapper, PagedDecodeWrapper) and wrapper.use_cuda_graph
         graph_static_pf = isinstance(wrapper, PagedPrefillWrapper) and wrapper.use_cuda_graph
         if graph_static or graph_static_pf:
@@ -222,16 +244,7 @@ class BatchedCacheManager:
             kv_indices = torch.empty(max(total_pages, 1), dtype=torch.int32, device=self.device)
             last = torch.empty(b, dtype=torch.int32, device=self.device)
         loc = torch.empty(b, 2, dtype=torch.long, device=self.device) if is_decode else None
-        grid = max(1, min(64, (total_pages + 8191) // 8192))
-        base = dmeta.data_ptr()
-        _lib.check(
-            _lib.lib().mi_pack(
-                base, base + 4 * b, base + 8 * b, base + 12 * b, b, bt.table.data_ptr(), bt.stride, ps_,
-                qo.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(), last.data_ptr(),
-                loc.data_ptr() if loc is not None else None, grid, _lib.stream_ptr(self.device),
-            ),
-            "mi_pack",
-        )
+        self._launch_pack(meta, qo, kv_indptr, kv_indices, last, loc)
         self._last_pack = (qo, kv_indptr, kv_indices[:total_pages], last, loc)
         if isinstance(wrapper, PagedDecodeWrapper):
             wrapper.plan(kv_indptr, kv_indices[:total_pages], last, kv_cache_locations=loc, dtype=dtype)
@@ -240,6 +253,113 @@ class BatchedCacheManager:
                                 causal=is_causal, dtype=dtype)
         ps.seq_lens = list(seq_lens)
         ps.write_store = write_store
+
+    # ------------------------------------------------------------ multi-label (CFG)
+    def plan_attention_batched_cfg(self, labels: list[str], seq_lens: list[int], is_causal: bool = False,
+                                   write_store: bool = False, dtype=torch.bfloat16,
+                                   combined_label: str = "_cfg_batched") -> None:
+        """One ragged batch over (label, request) pairs, label-major (``cache_manager.py:522-609``).
+
+        Each (label, request) pair is one entry with its own pages; all
+        entries are allocated in that order and packed by one GPU kernel,
+        then planned on a fresh prefill wrapper under ``combined_label``.
+        """
+        assert self.kv_cache is not None
+        cfg = self.kv_cache_config
+        entries = [(rid, label) for label in labels for rid in self.request_ids]
+        sls = [int(seq_lens[i]) for _ in labels for i in range(len(self.request_ids))]
+        meta = self._alloc_entries(entries, sls)
+        n = len(entries)
+        total_pages = int(meta[3].sum())
+        qo = torch.empty(n + 1, dtype=torch.int32, device=self.device)
+        kv_indptr = torch.empty(n + 1, dtype=torch.int32, device=self.device)
+        kv_indices = torch.empty(max(total_pages, 1), dtype=torch.int32, device=self.device)
+        last = torch.empty(n, dtype=torch.int32, device=self.device)
+        self._launch_pack(meta, qo, kv_indptr, kv_indices, last, None)
+        self._last_pack = (qo, kv_indptr, kv_indices[:total_pages], last, None)
+        wrapper = PagedPrefillWrapper(
+            workspace_buffer=self.buffer_manager.get(combined_label),
+            num_qo_heads=cfg.num_qo_heads,
+            num_kv_heads=cfg.num_kv_heads,
+            head_dim=cfg.head_dim,
+            page_size=cfg.page_size,
+            device=self.device,
+            enable_nvtx=self.enable_nvtx,
+        )
+        wrapper.plan_device(qo, kv_indptr, kv_indices[:total_pages], last, total_tokens=sum(sls),
+                            causal=is_causal, dtype=dtype)
+        self._plan_states[combined_label] = _PlanState(wrapper=wrapper, seq_lens=sls, write_store=write_store)
+
+    def plan_rope_batched_cfg(self, labels: list[str], seq_lens: list[int],
+                              per_label_pos_ids: dict[str, list[torch.Tensor]] | None = None,
+                              combined_label: str = "_cfg_batched") -> None:
+        """Position ids of the batched-CFG entries, label-major (``cache_manager.py:611-650``).
+
+        A label with explicit position tensors takes their concatenation; the
+        others count from each request's ``position_id_start`` for that label
+        (expanded on the GPU).  A label given an empty list counts too.
+        """
+        b = len(self.request_ids)
+        parts = []
+        for label in labels:
+            given = per_label_pos_ids.get(label) if per_label_pos_ids else None
+            if given:
+                parts.append(torch.cat([t.to(device=self.device, dtype=torch.long) for t in given]))
+                continue
+            meta = np.empty(2 * b + 1, dtype=np.int32)
+            meta[0] = 0
+            meta[1:b + 1] = np.cumsum(seq_lens, dtype=np.int64)
+            meta[b + 1:] = [self._get_state(rid, label).position_id_start for rid in self.request_ids]
+            n = int(meta[b]) if b else 0
+            out = torch.empty(n, dtype=torch.long, device=self.device)
+            if n:
+                dev = self._pack.upload(meta)
+                rope_positions(dev[: b + 1], dev[b + 1:], out, n)
+            parts.append(out)
+        self._plan_states[combined_label].pos_ids = parts[0] if len(parts) == 1 else torch.cat(parts)
+
+    def snapshot_all(self, from_label: str, to_label: str, realloc: bool = False, write_store: bool = True) -> None:
+        """Copy every request's KV history from one label to another (``cache_manager.py:840-870``).
+
+        Same page bookkeeping as the reference (the destination keeps its
+        first ``seq_len // page_size`` pages, grows to the source length,
+        takes its seq_len and position start); the page copies of all
+        requests and layers go to the GPU as one ``mi_copy_pages`` launch.
+        """
+        assert self.kv_cache is not None
+        ps_ = self.kv_cache_config.page_size
+        src, dst = [], []
+        for rid in self.request_ids:
+            from_state = self._get_state(rid, from_label)
+            if realloc:
+                self.alloc_manager.reset_label(rid, to_label)
+            to_state = self._get_state(rid, to_label)
+            start = to_state.seq_len // ps_
+            self.alloc_manager.alloc(rid, to_label, seq_len=from_state.seq_len)
+            to_state.seq_len = from_state.seq_len
+            to_state.position_id_start = from_state.position_id_start
+            a, b = from_state.page_indices[start:], to_state.page_indices[start:]
+            if len(a) != len(b):
+                raise ValueError(f"{rid}: {len(a)} source pages vs {len(b)} destination pages from page {start}")
+            src.extend(a)
+            dst.extend(b)
+            if write_store:
+                self.alloc_manager.flush_to_store(rid, label=to_label)
+        if src:
+            kv = self.kv_cache
+            page = kv[0, 0]
+            if not page.is_contiguous():
+                raise ValueError("snapshot_all needs each page of the KV pool to be contiguous")
+            esz = kv.element_size()
+            n = len(src)
+            dev = self._pack.upload(np.asarray(src + dst, dtype=np.int32))
+            _lib.check(
+                _lib.lib().mi_copy_pages(
+                    kv.data_ptr(), kv.stride(0) * esz, kv.shape[0], kv.stride(1) * esz, page.numel() * esz,
+                    kv.shape[1], dev.data_ptr(), dev.data_ptr() + 4 * n, n, _lib.stream_ptr(self.device),
+                ),
+                "mi_copy_pages",
+            )
 
     # ------------------------------------------------------------ running
     def _layer_scales(self, layer_idx: int):

@@ -152,3 +152,26 @@ def split_chunks(kv_indptr, page_size: int, target_units: int, num_kv_heads: int
     total = int(kv_indptr[-1] - kv_indptr[0])
     cp = max(-(-min_chunk_tokens // page_size), -(-total // target))
     return cp, np.where(npages > 0, -(-npages // cp), 0)
+
+
+def snapshot(from_state: ReqState, to_state: ReqState, pool: FifoPages, page_size: int,
+             cache=None, realloc: bool = False) -> tuple[ReqState, list[tuple[int, int]]]:
+    """``snapshot_all`` for one request (``mstar/engine/cache_manager.py:840-870``).
+
+    With ``realloc`` the destination's pages go back to the pool and it starts
+    empty.  The destination keeps its first ``seq_len // page_size`` pages,
+    grows to the source's length, takes its seq_len, and pages from there on
+    are copied source -> destination (all layers of ``cache [L, pages, ...]``
+    when given).  Returns the destination state and the (src, dst) pairs.
+    """
+    if realloc:
+        pool.give(to_state.pages)
+        to_state = ReqState()
+    start = to_state.seq_len // page_size
+    alloc(to_state, pool, from_state.seq_len, page_size)
+    to_state.seq_len = from_state.seq_len
+    pairs = list(zip(from_state.pages[start:], to_state.pages[start:], strict=True))
+    if cache is not None:
+        for s, d in pairs:
+            cache[:, d] = cache[:, s]
+    return to_state, pairs

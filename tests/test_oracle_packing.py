@@ -171,3 +171,41 @@ def test_split_chunks_cover_every_page_once():
         assert (k == 0) == (npg == 0)
         if npg:
             assert (k - 1) * cp < npg <= k * cp
+
+
+def test_snapshot_copies_history_and_keeps_leading_pages():
+    import torch
+
+    ps = 4
+    pool = P.FifoPages(40)
+    cache = torch.arange(40 * 3, dtype=torch.float32).reshape(1, 40, 3)  # one layer, 3 values per page
+    src = P.ReqState()
+    P.alloc(src, pool, 10, ps)
+    src.seq_len = 10
+    dst, pairs = P.snapshot(src, P.ReqState(), pool, ps, cache)
+    assert dst.seq_len == 10 and len(dst.pages) == 3 and set(dst.pages).isdisjoint(src.pages)
+    assert pairs == list(zip(src.pages, dst.pages))
+    assert torch.equal(cache[0, dst.pages], cache[0, src.pages])
+    # the source grows: only pages from dst.seq_len // ps on are copied again
+    P.alloc(src, pool, 19, ps)
+    src.seq_len = 19
+    cache[0, src.pages[2]] += 100.0  # the partially filled page changed
+    before = cache.clone()
+    dst, pairs = P.snapshot(src, dst, pool, ps, cache)
+    assert [s for s, _ in pairs] == src.pages[2:] and len(dst.pages) == 5
+    assert torch.equal(cache[0, dst.pages], cache[0, src.pages])
+    assert torch.equal(cache[0, dst.pages[:2]], before[0, dst.pages[:2]])  # leading pages untouched
+    # realloc returns the old pages to the pool first (FIFO tail) and copies everything
+    n_free = len(pool.free)
+    dst2, pairs = P.snapshot(src, dst, pool, ps, cache, realloc=True)
+    assert len(pairs) == 5 and len(pool.free) == n_free  # 5 freed, 5 taken
+    assert torch.equal(cache[0, dst2.pages], cache[0, src.pages])
+
+
+def test_snapshot_rejects_mismatched_page_counts():
+    pool = P.FifoPages(16)
+    src = P.ReqState()
+    P.alloc(src, pool, 20, 4)  # 5 pages for 20 tokens, but only 6 tokens counted as cached
+    src.seq_len = 6
+    with pytest.raises(ValueError):
+        P.snapshot(src, P.ReqState(), pool, 4)
