@@ -3,27 +3,29 @@
 // Replaces FlashInferPrefillWrapper.plan/run (mstar/utils/flashinfer_utils.py:162-269).
 //
 // plan:  token_map_kernel writes the per-new-token (page, slot) map of
-//        flashinfer_utils.py:211-256; prefill_plan_kernel lists the
-//        128-row tiles of every long-query request; short-query requests
+//        flashinfer_utils.py:211-256; prefill_plan_kernel lists the tiles of
+//        every long-query request, costs them, and cuts the (kv-head, tile)
+//        units into 8 cost-balanced per-XCD queues; short-query requests
 //        (qo_len * group <= 16, e.g. the decode rows of a mixed batch) get a
 //        split-KV plan for the decode kernel in the same workspace.
-// run:   decode kernel + merge for the short-query requests, then
-//        prefill_kernel for the tiles.
+// run:   mi_prefill_short (decode kernel + merge for the short-query
+//        requests) and mi_prefill_tiles (prefill_kernel).
 //
-// prefill_kernel: one workgroup = 4 wavefronts = 128 (query token, q-head)
-// rows of one request and one kv-head (GQA rows packed token-major, so K/V
-// are read once per group of q-heads).  Each wavefront owns 2 groups of 16
-// rows.  K/V tiles of 64 keys (32 for head_dim 256) are gathered from the
-// paged cache with 128-bit loads into registers one tile ahead, then stored
-// to LDS (rows padded by 16 bytes against bank conflicts) and shared by the
-// 4 wavefronts:
+// prefill_kernel (persistent, one workgroup per CU): a unit is a tile of
+// 256 (query token, q-head) rows (128 for head_dim 256) of one request and
+// kv-head -- GQA rows packed token-major, so K/V are read once per group of
+// q-heads -- and each of the 8 wavefronts owns 2 groups of 16 rows.  Keys go
+// in 32-key steps through a three-stage LDS ring filled from registers
+// loaded three steps ahead (page ids staged in LDS, so no load waits on an
+// index load):
 //   S^T[16 keys x 16 rows] = K . Q^T    (v_mfma_f32_16x16x32, K from LDS)
 //   online softmax in fp32 (exp2 domain), causal mask aligned to the end of the KV
-//   O^T[D x 16 rows]      += V^T . P^T  (v_mfma_f32_16x16x16, V transposed in registers)
+//   O^T[16 dims x 16 rows] += V^T . P^T (v_mfma_f32_16x16x32, V^T from the
+//                                        transposing LDS read ds_read_b64_tr_b16)
+// The two wavefronts of each SIMD run their softmax on opposite sides of
+// their MFMA work (ping-pong), so vector and matrix work overlap.
 // fp8 K/V are converted to the MFMA type when a tile is stored to LDS; the
 // per-head scales multiply the scores and the output.
-// Workgroups are mapped XCD-aware: the 8 XCDs each take a contiguous range of
-// (kv-head, tile) units, so the tiles of one request and head share an L2.
 #include "mi_common.h"
 #include "mi_internal.h"
 
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   constexpr int THREADS = C::THREADS, NL = C::NL, HALF = C::HALF, STAGE = C::STAGE;
   constexpr int LCH = FP8 ? 32 : 16;  // LDS bytes per loaded chunk
   constexpr float kNegInf = -__builtin_inff();
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * STAGE];
   __shared__ int32_t lds_pages[kPfPageCap];
 
   __shared__ int s_unit;
@@ -315,7 +317,8 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   const int key_cap = np * ps - 16;  // last 16-row group inside the request's pages
   int c0 = 0;  // first page of the page ids staged in LDS
   // NB register buffers (even): tile t+NB is loaded while tile t is computed
-  constexpr int NB = NL <= 2 ? 4 : 2;
+  // Three register buffers: tile i is loaded three steps before it is stored
+  constexpr int NB = 3;
   uint4 rr[NB][NL];
   auto load_tile = [&](int t, uint4 (&r)[NL]) {
 #pragma unroll
@@ -380,22 +383,33 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // index i of lane group grp stands for key 4*grp+i (i < 4) or 16+4*grp+i-4
   // (i >= 4): exactly the keys whose scores that lane holds, so P^T needs no
   // shuffle.
-  auto compute = [&](int t, int stage) {
+  auto qk = [&](int stage, f32x4 (&s)[2][2]) {
     const uint8_t* sk = lds + stage * STAGE;
-    const uint8_t* vt0 = sk + KEYS * RSK + (4 * grp + ((lane & 15) >> 2)) * RSV + 8 * (lane & 3);
-    const int kb = t * KEYS;
-    f32x4 s[2][2];
+    uint4 a[2][KS];
+#pragma unroll
+    for (int js = 0; js < 2; ++js)
+#pragma unroll
+      for (int st = 0; st < KS; ++st) a[js][st] = *(const uint4*)(sk + (16 * js + col) * RSK + (8 * grp + 32 * st) * 2);
 #pragma unroll
     for (int js = 0; js < 2; ++js) {
       s[0][js] = f32x4{0.f, 0.f, 0.f, 0.f};
       s[1][js] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int st = 0; st < KS; ++st) {
-        const uint4 a = *(const uint4*)(sk + (16 * js + col) * RSK + (8 * grp + 32 * st) * 2);
-        s[0][js] = MT::mma_16x16x32(a, qf[0][st], s[0][js]);
-        s[1][js] = MT::mma_16x16x32(a, qf[1][st], s[1][js]);
-      }
     }
+#pragma unroll
+    for (int st = 0; st < KS; ++st)
+#pragma unroll
+      for (int js = 0; js < 2; ++js) {
+        s[0][js] = MT::mma_16x16x32(a[js][st], qf[0][st], s[0][js]);
+        s[1][js] = MT::mma_16x16x32(a[js][st], qf[1][st], s[1][js]);
+      }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * KS, 0);  // all K fragment reads first
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * KS, 0);  // then the MFMAs
+  };
+  // Softmax in two parts: sm_max masks (tail tiles only), takes the row max
+  // and raises the running max when needed (a rare branch); sm_exp forms
+  // the probabilities and their row sums.
+  auto sm_max = [&](int t, f32x4 (&s)[2][2]) {
+    const int kb = t * KEYS;
     if (t >= t_mask) {  // wave-uniform: only the tiles that reach past some row's limit
 #pragma unroll
       for (int rg = 0; rg < 2; ++rg)
@@ -405,23 +419,32 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
           for (int r = 0; r < 4; ++r)
             if (kb + 16 * js + 4 * grp + r > lim[rg]) s[rg][js][r] = kNegInf;
     }
-    uint4 pb[2];
+    float mt[2];
+    bool grow[2];
 #pragma unroll
     for (int rg = 0; rg < 2; ++rg) {
-      float mt = kNegInf;
+      float m = kNegInf;
 #pragma unroll
       for (int js = 0; js < 2; ++js)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[rg][js][r]);
-      mt = rows4_max(mt);
-      const bool grow = mt > m_run[rg] + lazy_raw;
-      if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float alpha = grow ? fast_exp2((m_run[rg] - mt) * sl2) : 1.f;
-        if (grow) m_run[rg] = mt;
+        for (int r = 0; r < 4; ++r) m = fmaxf(m, s[rg][js][r]);
+      mt[rg] = rows4_max(m);
+      grow[rg] = mt[rg] > m_run[rg] + lazy_raw;
+    }
+    if (__builtin_amdgcn_ballot_w64(grow[0] || grow[1])) {
+#pragma unroll
+      for (int rg = 0; rg < 2; ++rg) {
+        const float alpha = grow[rg] ? fast_exp2((m_run[rg] - mt[rg]) * sl2) : 1.f;
+        if (grow[rg]) m_run[rg] = mt[rg];
         l_run[rg] *= alpha;
 #pragma unroll
         for (int jj = 0; jj < VW; ++jj) acc[rg][jj] *= alpha;
       }
+    }
+  };
+  auto sm_exp = [&](const f32x4 (&s)[2][2], uint4 (&pb)[2]) {
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg) {
       const float moff = m_run[rg] == kNegInf ? 0.f : -m_run[rg] * sl2;
       float pr[2][4];
 #pragma unroll
@@ -433,25 +456,39 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       // row sums of the rounded probabilities the PV product uses
       l_run[rg] = MT::sum2(pb[rg].w, MT::sum2(pb[rg].z, MT::sum2(pb[rg].y, MT::sum2(pb[rg].x, l_run[rg]))));
     }
-    // V^T fragments with the transposing LDS read: in each 16-lane group,
-    // lane j addresses row 4*grp + j/4 (+16 for MFMA k-slots 4..7) at dims
-    // 16*jj + 4*(j%4) .. +3, and lane l receives the group's 4 keys at dim
-    // 16*jj + l%16 -- the A operand of output tile jj (A row a = dim 16*jj + a).
+  };
+  // V^T fragments with the transposing LDS read: in each 16-lane group,
+  // lane j addresses row 4*grp + j/4 (+16 for MFMA k-slots 4..7) at dims
+  // 16*jj + 4*(j%4) .. +3, and lane l receives the group's 4 keys at dim
+  // 16*jj + l%16 -- the A operand of output tile jj (A row a = dim 16*jj + a).
+  auto pv = [&](int stage, const uint4 (&pb)[2]) {
+    const uint8_t* vt0 = lds + stage * STAGE + KEYS * RSK + (4 * grp + ((lane & 15) >> 2)) * RSV + 8 * (lane & 3);
+    uint4 a[VW];
 #pragma unroll
     for (int jj = 0; jj < VW; ++jj) {
       const v4i16 x0 = ds_read_tr16(vt0 + 32 * jj);
       const v4i16 x1 = ds_read_tr16(vt0 + 16 * RSV + 32 * jj);
       const uint2 a0 = bitcast<uint2>(x0), a1 = bitcast<uint2>(x1);
-      const uint4 a = make_uint4(a0.x, a0.y, a1.x, a1.y);
-      acc[0][jj] = MT::mma_16x16x32(a, pb[0], acc[0][jj]);
-      acc[1][jj] = MT::mma_16x16x32(a, pb[1], acc[1][jj]);
+      a[jj] = make_uint4(a0.x, a0.y, a1.x, a1.y);
     }
+#pragma unroll
+    for (int jj = 0; jj < VW; ++jj) {
+      acc[0][jj] = MT::mma_16x16x32(a[jj], pb[0], acc[0][jj]);
+      acc[1][jj] = MT::mma_16x16x32(a[jj], pb[1], acc[1][jj]);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * VW, 0);  // all V^T fragment reads first
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * VW, 0);  // then the MFMAs
   };
+  // Ping-pong: the two wavefronts that share a SIMD (one of waves {0,2,5,7},
+  // one of {1,3,4,6}, for either round-robin or paired wave placement) put
+  // their softmax on opposite sides of their MFMA work, so one's vector
+  // work runs under the other's matrix work.  Group A finishes tile T-1's
+  // softmax at the start of step T, group B finishes tile T's at its end.
+  const bool grp_a = ((wave ^ (wave >> 2)) & 1) == 0;
 
-  // ---- page chunks (one for contexts up to kPfPageCap pages); in each, a
-  // two-stage LDS ring fed from NB register buffers (loads run NB tiles
-  // ahead).  Loads past the last tile repeat the last tile, so the steady
-  // loop has no conditional loads and the compiler's vmcnt waits stay exact.
+  // ---- page chunks (one for contexts up to kPfPageCap pages).  Loads past
+  // the last tile repeat the last tile, so the steady loop has no
+  // conditional loads and the compiler's vmcnt waits stay exact.
   for (c0 = 0; c0 * ps < kv_end; c0 += kPfPageCap) {
     const int npg = min(np - c0, kPfPageCap);
     __syncthreads();
@@ -460,25 +497,55 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     const int t0 = c0 * ps / KEYS;
     const int t1 = min(n_kt, (c0 + kPfPageCap) * ps / KEYS);
     const int tl = t1 - 1;
-    // prologue: tiles t0 .. t0+NB-1 in flight, tile t0 in LDS stage 0
+    // Three-stage LDS ring: in step T both groups read V of tile T-1 (P.V)
+    // and K of tile T (scores), and tile T+1 is stored into the stage tile
+    // T-2 used.  Register buffer j holds the tiles t0 + j (mod 3), loaded
+    // three steps before they are stored.
+    const int n = t1 - t0;
 #pragma unroll
     for (int u = 0; u < NB; ++u) load_tile(min(t0 + u, tl), rr[u]);
     store_tile(t0, rr[0], 0);
+    load_tile(min(t0 + 3, tl), rr[0]);
     __syncthreads();
-    bool done = false;
-    for (int t = t0; !done; t += NB) {
+    f32x4 sc[2][2];
+    uint4 pbk[2];
+    // step 0: scores of tile t0; group B also its softmax
+    qk(0, sc);
+    if (!grp_a) {
+      sm_max(t0, sc);
+      sm_exp(sc, pbk);
+    }
+    store_tile(min(t0 + 1, tl), rr[1], 1);
+    load_tile(min(t0 + 4, tl), rr[1]);
+    __syncthreads();
+    // steps 1 .. n-1
+    for (int i = 1; i < n; i += 3) {
 #pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        load_tile(min(t + u + NB, tl), rr[u]);  // rr[u] held tile t+u, stored last step
-        compute(t + u, u & 1);
-        store_tile(min(t + u + 1, tl), rr[(u + 1) % NB], (u + 1) & 1);
-        __syncthreads();
-        if (t + u + 1 >= t1) {
-          done = true;
-          break;
+      for (int u = 0; u < 3; ++u) {
+        const int ii = i + u;
+        if (ii >= n) break;
+        const int T = t0 + ii;
+        if (grp_a) {
+          sm_max(T - 1, sc);
+          sm_exp(sc, pbk);
         }
+        pv(u % 3, pbk);            // stage of tile T-1 = (ii-1) % 3 = u
+        qk((u + 1) % 3, sc);       // stage of tile T = ii % 3
+        if (!grp_a) {
+          sm_max(T, sc);
+          sm_exp(sc, pbk);
+        }
+        store_tile(min(T + 1, tl), rr[(u + 2) % 3], (u + 2) % 3);
+        load_tile(min(T + 4, tl), rr[(u + 2) % 3]);
+        __syncthreads();
       }
     }
+    // last step: P.V of tile t1-1
+    if (grp_a) {
+      sm_max(t1 - 1, sc);
+      sm_exp(sc, pbk);
+    }
+    pv((n - 1) % 3, pbk);
   }
 
   // ---- epilogue: lane holds dims 16*jj + 4*grp + r of its row
