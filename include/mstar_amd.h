@@ -40,7 +40,7 @@ extern "C" {
 #define MI_ERR_WORKSPACE (-3)   /* workspace too small or not planned for this call */
 #define MI_ERR_LAUNCH (-4)      /* HIP launch error */
 
-#define MI_ABI_VERSION 1
+#define MI_ABI_VERSION 2
 
 /* One layer of the paged KV cache. Strides are in elements. */
 typedef struct mi_paged_kv {
@@ -68,25 +68,29 @@ int mi_abi_version(void);
  * P1 — per-step batch packing on the GPU.
  * Replaces the Python packing loop of BatchedCacheManager._plan_attention_impl
  * (mstar/engine/cache_manager.py:272-322).  Pages must already be allocated
- * (host FIFO allocator, mstar/engine/kv_store.py:463-482) and present in the
- * device block table.  For request r (batch order):
+ * (host FIFO allocator, mstar/engine/kv_store.py:463-482).  Request r's page
+ * list is its block-table row: the first table_pages[r] entries are already
+ * in the table, the remaining num_pages[r] - table_pages[r] follow in
+ * new_pages (all requests' new pages concatenated in batch order) and are
+ * written into the row by this call (table_pages == NULL: all pages are in
+ * the table, new_pages unused).  For request r (batch order):
  *   T_r             = seq_len[r] + new_len[r]
  *   qo_indptr[r+1]  = qo_indptr[r] + new_len[r]
  *   kv_indptr[r+1]  = kv_indptr[r] + num_pages[r]
- *   kv_indices[kv_indptr[r] + p] = block_table[req_slot[r] * block_table_stride + p]
+ *   kv_indices[kv_indptr[r] + p] = page p of request r's list
  *   last_page_len[r]= T_r % page_size, or page_size when that is 0
  *   kv_locations[r] = (last page of the request's list, last_page_len[r] - 1) when
  *                     new_len[r] == 1 (cache_manager.py:293-294), (-1, -1) if the list
  *                     is empty; only if kv_locations != NULL (int64 [batch, 2]); rows
  *                     with new_len != 1 are left untouched
  * grid_blocks: number of workgroups to launch (>= 1); every workgroup
- * recomputes the two prefix sums, so no inter-block synchronisation is needed.
+ * recomputes the prefix sums, so no inter-block synchronisation is needed.
  * ------------------------------------------------------------------------ */
 int mi_pack(const int32_t* req_slot, const int32_t* seq_len, const int32_t* new_len,
-            const int32_t* num_pages, int32_t batch, const int32_t* block_table,
-            int64_t block_table_stride, int32_t page_size, int32_t* qo_indptr,
-            int32_t* kv_indptr, int32_t* kv_indices, int32_t* last_page_len,
-            int64_t* kv_locations, int32_t grid_blocks, void* stream);
+            const int32_t* num_pages, int32_t batch, int32_t* block_table,
+            int64_t block_table_stride, const int32_t* table_pages, const int32_t* new_pages,
+            int32_t page_size, int32_t* qo_indptr, int32_t* kv_indptr, int32_t* kv_indices,
+            int32_t* last_page_len, int64_t* kv_locations, int32_t grid_blocks, void* stream);
 
 /* Incremental device block-table update: block_table[slot[i]*stride + pos[i]] = page[i]
  * for i < n.  Keeps the device copy of each request's page list in step with the

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_PATH = Path(__file__).resolve().parent / "libmstar_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # dtype codes (mstar_amd.h)
 MI_BF16 = 0
@@ -65,7 +65,7 @@ _F32 = ctypes.c_float
 SIGNATURES = {
     "mi_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "mi_abi_version": (ctypes.c_int, []),
-    "mi_pack": (ctypes.c_int, [_P, _P, _P, _P, _I32, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _P]),
+    "mi_pack": (ctypes.c_int, [_P, _P, _P, _P, _I32, _P, _I64, _P, _P, _I32, _P, _P, _P, _P, _P, _I32, _P]),
     "mi_block_table_update": (ctypes.c_int, [_P, _I64, _P, _P, _P, _I32, _P]),
     "mi_decode_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32]),
     "mi_decode_plan": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _I64, _P]),

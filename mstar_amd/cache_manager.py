@@ -164,14 +164,15 @@ class BatchedCacheManager:
 
     def _alloc_entries(self, entries: list[tuple[str, str]], seq_lens) -> np.ndarray:
         """FIFO allocation in batch order (``cache_manager.py:278-285``) and the pack
-        kernel's per-entry meta ``[slot | seq_len | new_len | num_pages]``.
+        kernel's input: per entry ``[slot | seq_len | new_len | num_pages | pages
+        already on the device]``, followed by the pages not yet on the device.
 
         Raises AllocationFailedError before any kernel is launched."""
         n = len(entries)
         if len(seq_lens) != n:
             raise ValueError(f"{len(seq_lens)} seq_lens for {n} requests")
         states = []
-        meta = np.empty((4, n), dtype=np.int32)
+        meta = np.empty((5, n), dtype=np.int32)
         for i, (rid, label) in enumerate(entries):
             st = self._get_state(rid, label)
             sl = int(seq_lens[i])
@@ -180,22 +181,25 @@ class BatchedCacheManager:
             meta[1, i] = st.seq_len
             meta[2, i] = sl
             meta[3, i] = len(st.page_indices)
-        self.alloc_manager.block_table.sync(states)
+        old, new_pages = self.alloc_manager.block_table.prepare(states)
         meta[0] = [st.slot for st in states]
-        return meta
+        meta[4] = old
+        return np.concatenate([meta.reshape(-1), new_pages])
 
     def _launch_pack(self, meta: np.ndarray, qo, kv_indptr, kv_indices, last, loc) -> None:
-        b = meta.shape[1]
-        total_pages = int(meta[3].sum())
-        dmeta = self._pack.upload(meta.reshape(-1))
+        """One upload of the step's metadata + new pages, one pack kernel."""
+        b = qo.shape[0] - 1
+        total_pages = int(meta[3 * b:4 * b].sum())
+        dmeta = self._pack.upload(meta)
         bt = self.alloc_manager.block_table
-        grid = max(1, min(64, (total_pages + 8191) // 8192))
+        grid = max(1, min(256, (total_pages + 1023) // 1024))  # about one page per thread
         base = dmeta.data_ptr()
         _lib.check(
             _lib.lib().mi_pack(
-                base, base + 4 * b, base + 8 * b, base + 12 * b, b, bt.table.data_ptr(), bt.stride,
-                self.kv_cache_config.page_size, qo.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(),
-                last.data_ptr(), loc.data_ptr() if loc is not None else None, grid, _lib.stream_ptr(self.device),
+                base, base + 4 * b, base + 8 * b, base + 12 * b, b, bt.table.data_ptr(), bt.stride, base + 16 * b,
+                base + 20 * b, self.kv_cache_config.page_size, qo.data_ptr(), kv_indptr.data_ptr(),
+                kv_indices.data_ptr(), last.data_ptr(), loc.data_ptr() if loc is not None else None, grid,
+                _lib.stream_ptr(self.device),
             ),
             "mi_pack",
         )
@@ -208,7 +212,7 @@ class BatchedCacheManager:
         ps_ = cfg.page_size
         b = len(self.request_ids)
         meta = self._alloc_entries([(rid, label) for rid in self.request_ids], seq_lens)
-        total_pages = int(meta[3].sum())
+        total_pages = int(meta[3 * b:4 * b].sum())
         is_decode = all(int(s) == 1 for s in seq_lens)
 
         ps = self._plan_states.get(label)
@@ -249,7 +253,7 @@ class BatchedCacheManager:
         if isinstance(wrapper, PagedDecodeWrapper):
             wrapper.plan(kv_indptr, kv_indices[:total_pages], last, kv_cache_locations=loc, dtype=dtype)
         else:
-            wrapper.plan_device(qo, kv_indptr, kv_indices[:total_pages], last, total_tokens=int(meta[2].sum()),
+            wrapper.plan_device(qo, kv_indptr, kv_indices[:total_pages], last, total_tokens=int(meta[2 * b:3 * b].sum()),
                                 causal=is_causal, dtype=dtype)
         ps.seq_lens = list(seq_lens)
         ps.write_store = write_store
@@ -270,7 +274,7 @@ class BatchedCacheManager:
         sls = [int(seq_lens[i]) for _ in labels for i in range(len(self.request_ids))]
         meta = self._alloc_entries(entries, sls)
         n = len(entries)
-        total_pages = int(meta[3].sum())
+        total_pages = int(meta[3 * n:4 * n].sum())
         qo = torch.empty(n + 1, dtype=torch.int32, device=self.device)
         kv_indptr = torch.empty(n + 1, dtype=torch.int32, device=self.device)
         kv_indices = torch.empty(max(total_pages, 1), dtype=torch.int32, device=self.device)

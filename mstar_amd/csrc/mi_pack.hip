@@ -3,15 +3,16 @@
 // Replaces the per-request Python loop of
 // BatchedCacheManager._plan_attention_impl (mstar/engine/cache_manager.py:272-322)
 // and its host->device copies.  Page ids stay owned by the host FIFO
-// allocator (mstar/engine/kv_store.py:25-67, 463-482); each newly allocated
-// page is written once into a device block table (mi_block_table_update),
-// and this kernel flattens the batch from that table every step.
+// allocator (mstar/engine/kv_store.py:25-67, 463-482); a device block table
+// keeps every live request's page list, and this kernel flattens the batch
+// from it every step.  Pages allocated since the previous step arrive with
+// the step's metadata and are written into the table by the same kernel.
 //
-// Every workgroup recomputes the two exclusive prefix sums (new tokens and
-// pages per request) in LDS, so the grid needs no inter-block
-// synchronisation; the flattening of kv_indices is then shared by all
-// workgroups (grid-stride over the batch's pages, one binary search in LDS
-// per page id).
+// Every workgroup recomputes the exclusive prefix sums (new tokens, pages
+// and newly sent pages per request) in LDS, so the grid needs no
+// inter-block synchronisation; the flattening of kv_indices is then shared
+// by all workgroups (grid-stride over the batch's pages, one binary search
+// in LDS per page id; the grid is sized for about one page per thread).
 #include "mi_common.h"
 #include "mi_internal.h"
 
@@ -24,7 +25,9 @@ struct PackParams {
   const int32_t* seq_len;
   const int32_t* new_len;
   const int32_t* num_pages;
-  const int32_t* block_table;
+  const int32_t* table_pages;  // leading pages already in the table (NULL: all)
+  const int32_t* new_pages;    // the rest, request by request
+  int32_t* block_table;
   int64_t bt_stride;
   int32_t* qo_indptr;
   int32_t* kv_indptr;
@@ -38,18 +41,24 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackParams p) {
   __shared__ int s_scan[16];
   __shared__ int s_off[kPackThreads + 1];  // window-relative exclusive page offsets
   __shared__ int s_slot[kPackThreads];
+  __shared__ int s_old[kPackThreads];      // pages of the request already in the table
+  __shared__ int s_noff[kPackThreads];     // window-relative offsets into new_pages
   const int tid = threadIdx.x;
-  int carry_qo = 0, carry_kv = 0;
+  int carry_qo = 0, carry_kv = 0, carry_new = 0;
   for (int base = 0; base < p.batch; base += kPackThreads) {
     const int b = base + tid;
     const bool live = b < p.batch;
     const int sl = live ? p.new_len[b] : 0;
     const int np = live ? p.num_pages[b] : 0;
-    int tot_qo, tot_kv;
+    const int old = live ? (p.table_pages ? min(p.table_pages[b], np) : np) : 0;
+    int tot_qo, tot_kv, tot_new;
     const int ex_qo = block_exclusive_scan_1024(sl, tot_qo, s_scan);
     const int ex_kv = block_exclusive_scan_1024(np, tot_kv, s_scan);
+    const int ex_new = block_exclusive_scan_1024(np - old, tot_new, s_scan);
     s_off[tid] = ex_kv;
     s_slot[tid] = live ? p.req_slot[b] : 0;
+    s_old[tid] = old;
+    s_noff[tid] = ex_new;
     if (tid == 0) s_off[kPackThreads] = tot_kv;
     if (blockIdx.x == 0 && live) {
       p.qo_indptr[b] = carry_qo + ex_qo;
@@ -62,7 +71,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackParams p) {
         // (last page of the request's list, last_page_len - 1): cache_manager.py:293-294
         int64_t page = -1, pos = -1;
         if (np > 0) {
-          page = p.block_table[(int64_t)s_slot[tid] * p.bt_stride + (np - 1)];
+          page = np - 1 < old ? p.block_table[(int64_t)s_slot[tid] * p.bt_stride + (np - 1)]
+                              : p.new_pages[carry_new + ex_new + (np - 1 - old)];
           pos = lpl - 1;
         }
         p.kv_locations[2 * b] = page;
@@ -70,7 +80,8 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackParams p) {
       }
     }
     __syncthreads();
-    // flatten this window's page lists: kv_indices[carry_kv + f] for f < tot_kv
+    // flatten this window's page lists: kv_indices[carry_kv + f] for f < tot_kv;
+    // pages past a request's table prefix come from new_pages and go into the table
     const int nreq = min(kPackThreads, p.batch - base);
     for (int f = blockIdx.x * kPackThreads + tid; f < tot_kv; f += gridDim.x * kPackThreads) {
       int lo = 0, hi = nreq - 1;  // last r with s_off[r] <= f
@@ -78,10 +89,20 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackParams p) {
         const int mid = (lo + hi + 1) >> 1;
         if (s_off[mid] <= f) lo = mid; else hi = mid - 1;
       }
-      p.kv_indices[carry_kv + f] = p.block_table[(int64_t)s_slot[lo] * p.bt_stride + (f - s_off[lo])];
+      const int j = f - s_off[lo];
+      int32_t* row = p.block_table + (int64_t)s_slot[lo] * p.bt_stride;
+      int page;
+      if (j < s_old[lo]) {
+        page = row[j];
+      } else {
+        page = p.new_pages[carry_new + s_noff[lo] + (j - s_old[lo])];
+        row[j] = page;
+      }
+      p.kv_indices[carry_kv + f] = page;
     }
     carry_qo += tot_qo;
     carry_kv += tot_kv;
+    carry_new += tot_new;
     __syncthreads();
   }
   if (blockIdx.x == 0 && tid == 0) {
@@ -100,20 +121,23 @@ __global__ __launch_bounds__(256) void block_table_update_kernel(int32_t* table,
 }  // namespace mi
 
 extern "C" int mi_pack(const int32_t* req_slot, const int32_t* seq_len, const int32_t* new_len,
-                       const int32_t* num_pages, int32_t batch, const int32_t* block_table,
-                       int64_t block_table_stride, int32_t page_size, int32_t* qo_indptr,
-                       int32_t* kv_indptr, int32_t* kv_indices, int32_t* last_page_len,
-                       int64_t* kv_locations, int32_t grid_blocks, void* stream) {
+                       const int32_t* num_pages, int32_t batch, int32_t* block_table,
+                       int64_t block_table_stride, const int32_t* table_pages, const int32_t* new_pages,
+                       int32_t page_size, int32_t* qo_indptr, int32_t* kv_indptr, int32_t* kv_indices,
+                       int32_t* last_page_len, int64_t* kv_locations, int32_t grid_blocks, void* stream) {
   using namespace mi;
   if (batch < 0 || page_size <= 0 || grid_blocks <= 0 || block_table_stride <= 0) return MI_ERR_INVALID;
   if (!qo_indptr || !kv_indptr || !last_page_len) return MI_ERR_INVALID;
   if (batch > 0 && (!req_slot || !seq_len || !new_len || !num_pages || !block_table || !kv_indices))
     return MI_ERR_INVALID;
+  if (table_pages && !new_pages) return MI_ERR_INVALID;
   PackParams pp;
   pp.req_slot = req_slot;
   pp.seq_len = seq_len;
   pp.new_len = new_len;
   pp.num_pages = num_pages;
+  pp.table_pages = table_pages;
+  pp.new_pages = new_pages;
   pp.block_table = block_table;
   pp.bt_stride = block_table_stride;
   pp.qo_indptr = qo_indptr;

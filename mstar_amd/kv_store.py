@@ -177,6 +177,28 @@ class DeviceBlockTable:
                 state._dev_list = None
                 state._dev_len = 0
 
+    def prepare(self, states: list[KVRequestState]) -> tuple[np.ndarray, np.ndarray]:
+        """What ``mi_pack`` must add to the table for ``states``: per state the
+        number of leading pages already on the device, and all the other pages
+        concatenated in order.  The caller hands both to the pack kernel, which
+        writes them into the table; the states are marked as synced."""
+        old = np.empty(len(states), dtype=np.int32)
+        parts = []
+        for i, st in enumerate(states):
+            self.acquire(st)
+            pl = st.page_indices
+            n = len(pl)
+            if n > self.stride:
+                raise ValueError(f"request holds {n} pages, block table rows hold {self.stride}")
+            start = st._dev_len if (st._dev_list is pl and n >= st._dev_len) else 0
+            old[i] = start
+            if n > start:
+                parts.append(pl[start:])
+            st._dev_list = pl
+            st._dev_len = n
+        new = np.fromiter((p for part in parts for p in part), dtype=np.int32) if parts else np.zeros(0, np.int32)
+        return old, new
+
     def sync(self, states: list[KVRequestState], stream: torch.cuda.Stream | None = None) -> None:
         """Bring the device rows of ``states`` up to date (async on ``stream``)."""
         slots, poss, pages = [], [], []

@@ -75,7 +75,7 @@ def test_workspace_sizes_are_host_arithmetic(L):
 def test_invalid_arguments_are_rejected_before_launch(L):
     nul = None
     # negative batch, null outputs
-    assert L.mi_pack(nul, nul, nul, nul, -1, nul, 0, 16, nul, nul, nul, nul, nul, 1, nul) == MI_ERR_INVALID
+    assert L.mi_pack(nul, nul, nul, nul, -1, nul, 0, nul, nul, 16, nul, nul, nul, nul, nul, 1, nul) == MI_ERR_INVALID
     assert L.mi_block_table_update(nul, 0, nul, nul, nul, 4, nul) == MI_ERR_INVALID
     # null workspace
     assert L.mi_decode_plan(nul, nul, nul, nul, 4, 16, 32, 4, 128, nul, nul, 0, nul) == MI_ERR_INVALID
