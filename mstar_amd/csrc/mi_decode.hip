@@ -271,8 +271,12 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   const int wave = uniform((int)threadIdx.x >> 6);
   const int nkv = p.num_kv_heads;
   // workgroup = (item, kv-head); its 4 waves split the item's tiles
-  const int item = uniform((int)blockIdx.x / nkv);
-  const int h = (int)blockIdx.x - item * nkv;
+  // all kv-heads of an item on one XCD (blocks go to XCDs round-robin), 8 blocks apart
+  const int gsz = 8 * nkv;
+  const int gi = uniform((int)blockIdx.x / gsz);
+  const int gr = (int)blockIdx.x - gi * gsz;
+  const int h = uniform(gr >> 3);
+  const int item = uniform(gi * 8 + (gr & 7));
   if (item >= p.hdr[kHdrChunks]) return;  // uniform across the workgroup
   const int4 wk = p.work[item];
   const int b = uniform(wk.x), kidx = uniform(wk.y), pg1 = uniform(wk.z), nitems_b = uniform(wk.w);
@@ -762,7 +766,7 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
   dp.page_size = kv->page_size;
   dp.causal = causal ? 1 : 0;
   dp.scale_log2 = sm_scale * 1.4426950408889634f;
-  const int grid = (int)(L.max_chunks * (int64_t)nkv);
+  const int grid = (int)((L.max_chunks + 7) / 8 * 8 * (int64_t)nkv);
   int st;
   if (q_dtype == MI_BF16)
     st = fp8 ? dispatch_d<BF16, true>(dp, D, grid, batch, phases, stream)
