@@ -335,6 +335,7 @@ def bench_decode(args, dev) -> dict:
         },
     }
     res["rope"] = bench_rope(q, k, np.array([cm._get_state(r).seq_len for r in rids]), args.steps)
+    res["kv_transfer"] = bench_transfer(kv, args.steps)
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
         res["cpu_baseline"] = cpu_baseline(bt, kv, q, k, v, cm.kv_scales)
@@ -374,6 +375,74 @@ def bench_rope(q, k, positions: np.ndarray, steps: int, per_graph: int = 20) -> 
     return {"kernel": "rope_kernel", "what": "apply_rope_pos_ids_inplace on the step's q [B, Hq, D] and k [B, Hkv, D], "
             f"{per_graph} launches per HIP graph replay", "kernel_us": us, "algorithmic_bytes": nbytes,
             "GBps": nbytes / (us * 1e-6) / 1e9}
+
+
+def bench_transfer(kv_layer: torch.Tensor, steps: int, pages: int = 32768, host_pages: int = 4096) -> dict:
+    """KV page transfer at the workload's page shape ``[2, ps, Hkv, D]``, one layer.
+
+    * ``mi_kv_copy_tokens``: ``pages`` whole pages from one pool to another,
+      random page ids on both sides (remote read / snapshot); HBM read + write;
+    * ``mi_kv_wire_pack``: the same pages into a contiguous wire buffer;
+    * ``mi_kv_copy_tokens`` into a pinned host pool (CPU offload), ``host_pages``
+      pages, bounded by the host link rather than HBM.
+    Records are uploaded before the timed launches; HIP events bracket
+    ``max(steps // 5, 5)`` launches each on the current stream.
+    """
+    import ctypes
+
+    from mstar_amd import _lib
+    from mstar_amd import kv_transfer as KT
+
+    if kv_layer.dim() == 6:  # [layers, pages, 2, ps, Hkv, D]
+        kv_layer = kv_layer[0]
+    dev = kv_layer.device
+    shape = (1, pages) + tuple(kv_layer.shape[1:])
+    bits = torch.uint8 if kv_layer.element_size() == 1 else torch.int16
+    src = torch.empty(shape, dtype=bits, device=dev)
+    src.random_(0, 127)
+    dst = torch.empty_like(src)
+    src, dst = src.view(kv_layer.dtype), dst.view(kv_layer.dtype)
+    host = torch.empty((1, host_pages) + tuple(kv_layer.shape[1:]), dtype=kv_layer.dtype, pin_memory=True)
+    g = torch.Generator().manual_seed(0)
+    rec = torch.stack([torch.randperm(pages, generator=g), torch.randperm(pages, generator=g)]).to(torch.int32).to(dev)
+    hrec = torch.arange(host_pages, dtype=torch.int32, device=dev)
+    page_bytes = src[0, 0].numel() * src.element_size()
+    wire = torch.empty(pages * page_bytes, dtype=torch.uint8, device=dev)
+    sd, dd, hd = KT.pool_desc(src), KT.pool_desc(dst), KT.pool_desc(host)
+    L = _lib.lib()
+    st = _lib.stream_ptr(dev)
+    d0, s0 = rec.data_ptr(), rec.data_ptr() + 4 * pages
+
+    def copy():
+        return L.mi_kv_copy_tokens(ctypes.byref(sd), ctypes.byref(dd), s0, d0, None, None, pages, 0, 1, st)
+
+    def pack():
+        return L.mi_kv_wire_pack(ctypes.byref(sd), s0, None, None, None, pages, 0, 1, wire.data_ptr(), wire.numel(), st)
+
+    def offload():
+        return L.mi_kv_copy_tokens(ctypes.byref(sd), ctypes.byref(hd), s0, hrec.data_ptr(), None, None, host_pages,
+                                   0, 1, st)
+
+    n = max(steps // 5, 5)
+    out = {"kernel": "kv_segments_kernel", "page_bytes": page_bytes,
+           "what": f"{pages} random whole pages pool->pool and pool->wire, {host_pages} pages pool->pinned host"}
+    for name, fn, moved, count_both in (("copy", copy, pages * page_bytes, True),
+                                        ("wire_pack", pack, pages * page_bytes, True),
+                                        ("offload_to_host", offload, host_pages * page_bytes, False)):
+        for _ in range(3):
+            _lib.check(fn(), name)
+        evs = _kernel_events(n, 2)
+        for e0, e1 in evs:
+            e0.record()
+            _lib.check(fn(), name)
+            e1.record()
+        torch.cuda.synchronize()
+        us = float(np.median([a.elapsed_time(b) for a, b in evs])) * 1e3
+        nbytes = moved * (2 if count_both else 1)
+        out[name] = {"kernel_us_median": us, "algorithmic_bytes": nbytes, "GBps": nbytes / (us * 1e-6) / 1e9}
+        if count_both:
+            out[name]["hbm_frac"] = out[name]["GBps"] / HBM_PEAK_GBS
+    return out
 
 
 def prefill_flops(bt) -> tuple[int, int]:

@@ -251,7 +251,7 @@ int mi_rope_apply(void* q, int64_t q_stride_token, int64_t q_stride_head, int32_
                   void* stream);
 
 /* ------------------------------------------------------------------------
- * Page snapshot copies (the path's next row: multi-label / CFG planning).
+ * Page snapshot copies (multi-label / CFG planning).
  * mi_copy_pages replaces the per-page copies of BatchedCacheManager.snapshot_all
  * (mstar/engine/cache_manager.py:840-870): for i < num_pairs and every layer l,
  *   page dst_pages[i] of layer l := page src_pages[i] of layer l
@@ -262,6 +262,67 @@ int mi_rope_apply(void* q, int64_t q_stride_token, int64_t q_stride_head, int32_
 int mi_copy_pages(void* pool, int64_t layer_stride_bytes, int32_t num_layers, int64_t page_stride_bytes,
                   int64_t page_bytes, int64_t max_pages, const int32_t* src_pages, const int32_t* dst_pages,
                   int32_t num_pairs, void* stream);
+
+/* ------------------------------------------------------------------------
+ * KV page transfer: remote reads, CPU offload/reload, wire format.
+ *
+ * A whole KV pool, all layers: [num_layers][num_pages][2 (K,V)][page_size]
+ * token rows of token_stride bytes (num_kv_heads * head_dim elements, the
+ * layout of kv_cache_engine.py:132-136), byte strides, 16-byte aligned.
+ * `data` must be HIP device memory or HIP-allocated pinned host memory
+ * (torch pin_memory); anything else is MI_ERR_INVALID.
+ *
+ * A record i names a page and a token range [token_start[i], token_end[i])
+ * (NULL arrays: whole pages) and stands for the K rows and the V rows of
+ * that range in every layer of [layer_begin, layer_end).  Records with page
+ * ids outside [0, num_pages) or an empty or out-of-page range are skipped.
+ * No destination row may be written by two records or read by another
+ * record of the same call.
+ * ------------------------------------------------------------------------ */
+typedef struct mi_kv_pool {
+  void* data;           /* (layer 0, page 0, K, token 0) */
+  int64_t layer_stride; /* bytes */
+  int64_t page_stride;  /* bytes */
+  int64_t kv_stride;    /* bytes from a page's K half to its V half */
+  int64_t token_stride; /* bytes of one token row; rows of a half are contiguous */
+  int64_t num_pages;
+  int32_t num_layers;
+  int32_t page_size;
+} mi_kv_pool;
+
+/* Pool-to-pool token copies: dst page dst_pages[i] rows [ts, te) := src page
+ * src_pages[i] rows [ts, te), K and V, every layer of the range.  src and
+ * dst may be the same pool (then sources and destinations must not overlap)
+ * and either may live in pinned host memory.  Replaces
+ *   - CudaIpcKVTransferEngine._do_read (mstar/engine/kv_store.py:330-380) and
+ *     MooncakeKVTransferEngine.read_batched_async + _get_ptr_nbytes
+ *     (kv_store.py:233-285): one KVReadInfo per (layer, page), one transfer
+ *     or torch copy per record;
+ *   - CPUPagePool.offload_pages / reload_pages
+ *     (mstar/engine/cpu_page_pool.py:63-124): one torch copy per page.
+ * src and dst must agree in token_stride and page_size. */
+int mi_kv_copy_tokens(const mi_kv_pool* src, const mi_kv_pool* dst, const int32_t* src_pages,
+                      const int32_t* dst_pages, const int32_t* token_start, const int32_t* token_end,
+                      int32_t num_records, int32_t layer_begin, int32_t layer_end, void* stream);
+
+/* Wire format: the records' rows in one contiguous buffer, layer-major.  With
+ * rows_i = token_end[i] - token_start[i], R = sum rows_i and row_offset the
+ * exclusive prefix sum of rows (num_records + 1 entries, device memory;
+ * NULL allowed only with NULL token ranges, meaning i * page_size), record
+ * i's K rows for layer l start at token row
+ *   2*R*(l - layer_begin) + 2*row_offset[i]
+ * followed by its V rows; the buffer holds
+ * 2*R*(layer_end - layer_begin)*token_stride bytes.  Segments that would fall
+ * outside [0, wire_bytes) or whose row_offset entries disagree with the
+ * ranges are skipped.  No counterpart in the reference, which moves each
+ * (layer, page, K|V) segment separately (kv_store.py:261-285); a transport
+ * sends one buffer instead. */
+int mi_kv_wire_pack(const mi_kv_pool* pool, const int32_t* pages, const int32_t* token_start,
+                    const int32_t* token_end, const int64_t* row_offset, int32_t num_records,
+                    int32_t layer_begin, int32_t layer_end, void* wire, int64_t wire_bytes, void* stream);
+int mi_kv_wire_unpack(const void* wire, int64_t wire_bytes, const mi_kv_pool* pool, const int32_t* pages,
+                      const int32_t* token_start, const int32_t* token_end, const int64_t* row_offset,
+                      int32_t num_records, int32_t layer_begin, int32_t layer_end, void* stream);
 
 #ifdef __cplusplus
 }

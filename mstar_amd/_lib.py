@@ -56,6 +56,21 @@ class MiPagedKV(ctypes.Structure):
     ]
 
 
+class MiKvPool(ctypes.Structure):
+    """Mirror of ``mi_kv_pool`` (mstar_amd.h)."""
+
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("layer_stride", ctypes.c_int64),
+        ("page_stride", ctypes.c_int64),
+        ("kv_stride", ctypes.c_int64),
+        ("token_stride", ctypes.c_int64),
+        ("num_pages", ctypes.c_int64),
+        ("num_layers", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+    ]
+
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
@@ -110,6 +125,18 @@ SIGNATURES = {
     ),
     "mi_rope_positions": (ctypes.c_int, [_P, _P, _I32, _P, _I32, _P]),
     "mi_copy_pages": (ctypes.c_int, [_P, _I64, _I32, _I64, _I64, _I64, _P, _P, _I32, _P]),
+    "mi_kv_copy_tokens": (
+        ctypes.c_int,
+        [ctypes.POINTER(MiKvPool), ctypes.POINTER(MiKvPool), _P, _P, _P, _P, _I32, _I32, _I32, _P],
+    ),
+    "mi_kv_wire_pack": (
+        ctypes.c_int,
+        [ctypes.POINTER(MiKvPool), _P, _P, _P, _P, _I32, _I32, _I32, _P, _I64, _P],
+    ),
+    "mi_kv_wire_unpack": (
+        ctypes.c_int,
+        [_P, _I64, ctypes.POINTER(MiKvPool), _P, _P, _P, _P, _I32, _I32, _I32, _P],
+    ),
     "mi_rope_apply": (
         ctypes.c_int,
         [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _I32, _I32, _I32, _F32, _F32,

@@ -7,10 +7,15 @@ Host side mirrors M*'s ``mstar/engine/kv_store.py``:
   tail.  Page ids therefore depend on batch order exactly as in the reference.
 * :class:`KVCacheConfig`, :class:`KVRequestState`, :class:`AllocationFailedError`
   (``kv_store.py:70-154``).
-* :class:`PagedAllocationManager` — the subset of ``kv_store.py:394-614`` that
-  the attention path uses (``alloc``, ``get_state``, ``add_request``,
-  ``remove_request``, ``reset_label``).  Remote transfer engines, CPU offload
-  and the distributed store are outside this library.
+* :class:`PagedAllocationManager` — ``kv_store.py:394-660``: allocation and
+  request state (``alloc``, ``get_state``, ``add_request``, ``remove_request``,
+  ``reset_label``), remote reads (``start_async_retrieve``, ``sync_retrieve``,
+  ``check_retrieve_ready``, ``get_per_label_seq_info``, through
+  :class:`mstar_amd.kv_transfer.DeviceKVTransferEngine`) and CPU offload
+  (``offload_request`` / ``reload_request`` with
+  :class:`mstar_amd.kv_transfer.CPUPagePool`).  The Mooncake/RDMA transport
+  and the distributed store are outside this library; a transport moves
+  the buffers of :func:`mstar_amd.kv_transfer.pack_wire`.
 
 Device side (new): :class:`DeviceBlockTable` keeps a copy of every request's
 page list in HBM (``int32 [slots, max_pages_per_seq]``).  Only pages allocated
@@ -255,8 +260,9 @@ class PagedAllocationManager:
     """
 
     def __init__(self, config: KVCacheConfig, kv_cache: torch.Tensor | None = None,
-                 device: torch.device | str | None = None):
+                 device: torch.device | str | None = None, transfer_engine=None):
         self.config = config
+        self._kv_transfer_engine = transfer_engine
         self.page_allocator = PageAllocator(config.max_num_pages)
         self.request_states: dict[str, dict[str, KVRequestState]] = {}
         self.kv_cache = kv_cache
@@ -313,6 +319,7 @@ class PagedAllocationManager:
         return list(self.request_states[request_id].keys())
 
     def reset_label(self, request_id: str, label: str, free: bool = True) -> None:
+        self.wait_for_retrieves(request_id, label)
         with self._lock:
             old = self.request_states[request_id].get(label)
             if old is not None:
@@ -329,6 +336,8 @@ class PagedAllocationManager:
             self.pending_reads[request_id] = {label: [] for label in labels}
 
     def remove_request(self, request_id: str) -> None:
+        for label in self.request_states[request_id]:
+            self.wait_for_retrieves(request_id, label)
         with self._lock:
             for state in self.request_states[request_id].values():
                 self.page_allocator.free(state.page_indices)
@@ -336,3 +345,120 @@ class PagedAllocationManager:
                     self.block_table.release(state)
             del self.request_states[request_id]
             del self.pending_reads[request_id]
+
+    # ----- remote reads (kv_store.py:484-581) -----
+
+    @property
+    def kv_transfer_engine(self):
+        """The engine remote reads go through; built over ``kv_cache`` on first use."""
+        if self._kv_transfer_engine is None:
+            from .kv_transfer import DeviceKVTransferEngine
+
+            if self.kv_cache is None:
+                raise RuntimeError("remote KV reads need the manager's kv_cache")
+            self._kv_transfer_engine = DeviceKVTransferEngine(self.kv_cache)
+        return self._kv_transfer_engine
+
+    def wait_for_retrieves(self, request_id: str, label: str) -> None:
+        for future in self.pending_reads.get(request_id, {}).get(label, []):
+            future.result()
+        if label in self.request_states.get(request_id, {}):
+            self.request_states[request_id][label].read_in_progress = False
+        if request_id in self.pending_reads:
+            self.pending_reads[request_id][label] = []
+
+    def check_retrieve_ready(self, request_id: str, label: str) -> bool:
+        """True once every read of (request, label) has finished (``kv_store.py:493-509``)."""
+        state = self.get_state(request_id, label)
+        if not state.read_in_progress:
+            return True
+        futures = [f for f in self.pending_reads[request_id].get(label, []) if not f.done()]
+        state.read_in_progress = len(futures) > 0
+        self.pending_reads[request_id][label] = futures
+        return not state.read_in_progress
+
+    def sync_retrieve(self, request_id: str, label: str, seq_info) -> None:
+        self.start_async_retrieve(request_id, label, seq_info)
+        self.wait_for_retrieves(request_id, label)
+
+    def start_async_retrieve(self, request_id: str, label: str, seq_info) -> None:
+        """Read the producer's tokens [local seq_len, seq_info.seq_len) (``kv_store.py:515-566``).
+
+        Same page and token ranges as the reference; all layers of all pages
+        go out as one launch on the engine's transfer stream.  The producer
+        must have finished writing those pages (the reference's contract,
+        ``kv_store.py:548-554``).
+        """
+        seq_len = seq_info.seq_len
+        state = self.get_state(request_id, label)
+        if state.seq_len >= seq_len:
+            return
+        ps = self.config.page_size
+        first = state.seq_len // ps
+        last = (seq_len - 1) // ps
+        self.alloc(request_id, label, seq_len)
+        n = last - first + 1
+        ts = np.zeros(n, np.int64)
+        ts[0] = state.seq_len % ps
+        te = np.full(n, ps, np.int64)
+        te[-1] = seq_len % ps or ps
+        local = np.asarray(state.page_indices[first:last + 1], dtype=np.int64)
+        remote = np.asarray(seq_info.page_indices[first:last + 1], dtype=np.int64)
+        if remote.size != n:
+            raise ValueError(f"producer lists {len(seq_info.page_indices)} pages for {seq_len} tokens")
+        future = self.kv_transfer_engine.read_pages_async(seq_info.latest_kv_transfer_info, local, remote, ts, te)
+        if future is not None:
+            self.pending_reads[request_id].setdefault(label, []).append(future)
+        state.seq_len = seq_len
+        state.position_id_start = seq_info.pos_id
+        state.read_in_progress = future is not None
+
+    def get_per_label_seq_info(self, request_id: str) -> dict:
+        """What a consumer needs to read every label of a request (``kv_store.py:568-581``)."""
+        from .kv_transfer import SequenceInfo
+
+        info = self.kv_transfer_engine.get_kv_transfer_info()
+        out = {}
+        for label in list(self.request_states.get(request_id, {})):
+            self.wait_for_retrieves(request_id, label)
+            st = self.get_state(request_id, label)
+            out[label] = SequenceInfo(seq_len=st.seq_len, pos_id=st.position_id_start,
+                                      latest_kv_transfer_info=info, page_indices=st.page_indices)
+        return out
+
+    # ----- CPU offloading (kv_store.py:617-660) -----
+
+    def offload_request(self, request_id: str, cpu_pool) -> int:
+        """Offload every label of a request to ``cpu_pool`` and free its GPU pages.
+
+        As in the reference, a label whose CPU pages run out is not recorded
+        by the pool but its GPU pages are still freed.
+        """
+        freed = 0
+        with self._lock:
+            labels = list(self.request_states[request_id].items())
+        for label, state in labels:
+            if not state.page_indices:
+                continue
+            self.wait_for_retrieves(request_id, label)
+            cpu_pool.offload_pages(request_id, label, self.kv_cache, state.page_indices, state.seq_len,
+                                   state.position_id_start)
+            with self._lock:
+                freed += len(state.page_indices)
+                self.page_allocator.free(state.page_indices)
+                state.page_indices = []
+                state.seq_len = 0
+        return freed
+
+    def reload_request(self, request_id: str, cpu_pool) -> None:
+        """Reload every offloaded label of a request into fresh GPU pages (``RuntimeError`` when short)."""
+        with self._lock:
+            for label in list(cpu_pool.offloaded.get(request_id, {}).keys()):
+                n = len(cpu_pool.offloaded[request_id][label].cpu_page_indices)
+                pages = self.page_allocator.allocate(n)
+                state = self.get_state(request_id, label)
+                state.page_indices = pages
+                seq_len, pos = cpu_pool.reload_pages(request_id, label, self.kv_cache, pages)
+                state.seq_len = seq_len
+                state.position_id_start = pos
+        cpu_pool.sync()

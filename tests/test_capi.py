@@ -108,3 +108,31 @@ def test_rope_arguments_are_checked(L):
                            None) == MI_ERR_INVALID
     assert L.mi_rope_positions(None, None, 0, None, 5, None) == MI_ERR_INVALID
     assert L.mi_rope_positions(None, None, 0, None, 0, None) == 0
+
+
+def test_transfer_arguments_are_checked(L):
+    """KV transfer: malformed pool descriptors and ranges fail before any HIP call."""
+    buf = (ctypes.c_int32 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+
+    def pool(**kw):
+        d = _lib.MiKvPool()
+        d.data, d.layer_stride, d.page_stride, d.kv_stride, d.token_stride = 4096, 1 << 20, 1 << 14, 1 << 13, 512
+        d.num_pages, d.num_layers, d.page_size = 16, 2, 16
+        for k, v in kw.items():
+            setattr(d, k, v)
+        return ctypes.byref(d)
+
+    bad = [pool(data=None), pool(token_stride=0), pool(page_stride=24), pool(data=4100), pool(kv_stride=256),
+           pool(num_layers=0)]
+    for b in bad:
+        assert L.mi_kv_copy_tokens(b, b, p, p, None, None, 1, 0, 1, None) == MI_ERR_INVALID
+        assert L.mi_kv_wire_pack(b, p, None, None, None, 1, 0, 1, p, 64, None) == MI_ERR_INVALID
+        assert L.mi_kv_wire_unpack(p, 64, b, p, None, None, None, 1, 0, 1, None) == MI_ERR_INVALID
+    good = pool()
+    assert L.mi_kv_copy_tokens(None, good, p, p, None, None, 1, 0, 1, None) == MI_ERR_INVALID
+    # layer range past the pool, negative record count, one-sided token range
+    assert L.mi_kv_copy_tokens(good, good, p, p, None, None, 1, 0, 3, None) == MI_ERR_INVALID
+    assert L.mi_kv_copy_tokens(good, good, p, p, None, None, -1, 0, 1, None) == MI_ERR_INVALID
+    assert L.mi_kv_copy_tokens(good, good, p, p, p, None, 1, 0, 1, None) == MI_ERR_INVALID
+    assert L.mi_kv_wire_pack(good, p, p, None, None, 1, 0, 1, p, 64, None) == MI_ERR_INVALID
