@@ -423,12 +423,18 @@ def bench_transfer(kv_layer: torch.Tensor, steps: int, pages: int = 32768, host_
         return L.mi_kv_copy_tokens(ctypes.byref(sd), ctypes.byref(hd), s0, hrec.data_ptr(), None, None, host_pages,
                                    0, 1, st)
 
+    def device_copy():  # contiguous torch copy of the same bytes: what a plain HBM copy reaches
+        dst.view(-1).copy_(src.view(-1))
+        return 0
+
     n = max(steps // 5, 5)
     out = {"kernel": "kv_segments_kernel", "page_bytes": page_bytes,
-           "what": f"{pages} random whole pages pool->pool and pool->wire, {host_pages} pages pool->pinned host"}
+           "what": f"{pages} random whole pages pool->pool and pool->wire, {host_pages} pages pool->pinned host; "
+                   "torch_contiguous_copy = dst.copy_(src) of the same bytes, for scale"}
     for name, fn, moved, count_both in (("copy", copy, pages * page_bytes, True),
                                         ("wire_pack", pack, pages * page_bytes, True),
-                                        ("offload_to_host", offload, host_pages * page_bytes, False)):
+                                        ("offload_to_host", offload, host_pages * page_bytes, False),
+                                        ("torch_contiguous_copy", device_copy, pages * page_bytes, True)):
         for _ in range(3):
             _lib.check(fn(), name)
         evs = _kernel_events(n, 2)
