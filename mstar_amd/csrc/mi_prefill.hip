@@ -17,7 +17,8 @@
 // q-heads -- and each of the 8 wavefronts owns 2 groups of 16 rows.  Keys go
 // in 32-key steps through a three-stage LDS ring filled from registers
 // loaded three steps ahead (page ids staged in LDS, so no load waits on an
-// index load):
+// index load); a tile's V^T fragments are read in the step that computes its
+// scores and consumed by the next step's P.V MFMAs:
 //   S^T[16 keys x 16 rows] = K . Q^T    (v_mfma_f32_16x16x32, K from LDS)
 //   online softmax in fp32 (exp2 domain), causal mask aligned to the end of the KV
 //   O^T[16 dims x 16 rows] += V^T . P^T (v_mfma_f32_16x16x32, V^T from the
@@ -39,16 +40,18 @@ constexpr int kPfKeys = 32;                // keys per K/V tile
 constexpr int kPfPageCap = 2048;           // page ids staged in LDS at a time
 constexpr int kShortRows = 16;  // qo_len * group <= 16 -> decode kernel
 
-// Workspace: header | per-XCD queue counters | tile list | tile cost prefix | decode split plan.
+// Workspace: header | per-XCD queue counters | tile list | tile cost prefix |
+// unit order | decode split plan.
 // Header words: [0] tiles, [1] units (tiles x kv-heads), [8 + x] first unit
 // of XCD x's queue (x = 0..8, [16] = units).
 struct PrefillLayout {
-  int64_t hdr, ctr, tiles, tcum, split;
+  int64_t hdr, ctr, tiles, tcum, order, split;
   int32_t max_tiles;
 };
 constexpr int kCtrStride = 32;  // one 128-byte line per XCD counter
 
-static PrefillLayout prefill_layout(int32_t batch, int32_t max_qo_tokens, int32_t group, int32_t head_dim) {
+static PrefillLayout prefill_layout(int32_t batch, int32_t max_qo_tokens, int32_t group, int32_t nkv,
+                                    int32_t head_dim) {
   const int tile_rows = pf_rows(head_dim);
   PrefillLayout L;
   const int64_t rows = (int64_t)max_qo_tokens * group;
@@ -59,7 +62,8 @@ static PrefillLayout prefill_layout(int32_t batch, int32_t max_qo_tokens, int32_
   L.ctr = 256;
   L.tiles = L.ctr + 8 * kCtrStride * 4;
   L.tcum = mi_align_up(L.tiles + 8LL * L.max_tiles, 256);
-  L.split = mi_align_up(L.tcum + 4LL * (L.max_tiles + 1), 256);
+  L.order = mi_align_up(L.tcum + 4LL * (L.max_tiles + 1), 256);
+  L.split = mi_align_up(L.order + 4LL * L.max_tiles * nkv, 256);
   return L;
 }
 
@@ -101,7 +105,8 @@ __global__ __launch_bounds__(256) void token_map_kernel(const int32_t* qo_indptr
 // A tile's cost is its number of 32-key steps.  Units (kv-head, tile) in
 // head-major order are cut into 8 contiguous runs of equal cost, one queue
 // per XCD, so each XCD's L2 serves few (request, head) KV streams and the
-// XCDs finish together.
+// XCDs finish together; within a queue the units are taken heaviest first
+// (longest-processing-time order), so the kernel's tail holds short units.
 __device__ int pf_tile_cost(int kv_len, int qo_len, int rows_total, int row0, int tile_rows, int group,
                             int causal) {
   const int last_row = min(row0 + tile_rows, rows_total) - 1;
@@ -113,8 +118,11 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* qo_in
                                                             const int32_t* last_page_len, int32_t batch,
                                                             int32_t page_size, int32_t group, int32_t nkv,
                                                             int32_t tile_rows, int32_t max_tiles, int32_t causal,
-                                                            int32_t* hdr, int2* tiles, int32_t* tcum) {
+                                                            int32_t* hdr, int2* tiles, int32_t* tcum,
+                                                            int32_t* order) {
   __shared__ int smem[16];
+  __shared__ int s_cut[9];
+  __shared__ int s_bin[1024];
   int carry = 0, carry_cost = 0;
   for (int base = 0; base < batch; base += 1024) {
     const int b = base + (int)threadIdx.x;
@@ -166,6 +174,30 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* qo_in
       u0 = lo;
     }
     hdr[8 + x] = (int32_t)u0;
+    s_cut[x] = (int)u0;
+  }
+  __syncthreads();
+  // Within each queue, units go heaviest first (counting sort by cost,
+  // clamped to 1023 steps), so the tail of the kernel runs the short ones.
+  for (int x = 0; x < 8; ++x) {
+    const int lo = s_cut[x], hi = s_cut[x + 1];
+    s_bin[threadIdx.x] = 0;
+    __syncthreads();
+    for (int u = lo + (int)threadIdx.x; u < hi; u += 1024) {
+      const int t = u % n_tiles;
+      atomicAdd(&s_bin[1023 - min(tcum[t + 1] - tcum[t], 1023)], 1);
+    }
+    __syncthreads();
+    int tot;
+    const int start = block_exclusive_scan_1024(s_bin[threadIdx.x], tot, smem) + lo;
+    __syncthreads();
+    s_bin[threadIdx.x] = start;
+    __syncthreads();
+    for (int u = lo + (int)threadIdx.x; u < hi; u += 1024) {
+      const int t = u % n_tiles;
+      order[atomicAdd(&s_bin[1023 - min(tcum[t + 1] - tcum[t], 1023)], 1)] = u;
+    }
+    __syncthreads();
   }
 }
 
@@ -187,6 +219,7 @@ struct PrefillParams {
   const int32_t* last_page_len;
   const int32_t* hdr;
   const int2* tiles;
+  const int32_t* order;
   int32_t* ctr;
   void* out;
   int64_t out_stride_tok, out_stride_head;
@@ -238,7 +271,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       if (len <= 0 || __hip_atomic_load(p.ctr + y * kCtrStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= len)
         continue;
       const int i = atomicAdd(p.ctr + y * kCtrStride, 1);
-      if (i < len) u = first + i;
+      if (i < len) u = p.order[first + i];
     }
     s_unit = u;
   }
@@ -461,9 +494,11 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // lane j addresses row 4*grp + j/4 (+16 for MFMA k-slots 4..7) at dims
   // 16*jj + 4*(j%4) .. +3, and lane l receives the group's 4 keys at dim
   // 16*jj + l%16 -- the A operand of output tile jj (A row a = dim 16*jj + a).
-  auto pv = [&](int stage, const uint4 (&pb)[2]) {
+  // The fragments of tile T are read in the step that computes its scores
+  // and kept in registers across the barrier: the P.V MFMAs of the next
+  // step then start without waiting on LDS, while that step's K reads run.
+  auto vfrag = [&](int stage, uint4 (&a)[VW]) {
     const uint8_t* vt0 = lds + stage * STAGE + KEYS * RSK + (4 * grp + ((lane & 15) >> 2)) * RSV + 8 * (lane & 3);
-    uint4 a[VW];
 #pragma unroll
     for (int jj = 0; jj < VW; ++jj) {
       const v4i16 x0 = ds_read_tr16(vt0 + 32 * jj);
@@ -471,13 +506,13 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       const uint2 a0 = bitcast<uint2>(x0), a1 = bitcast<uint2>(x1);
       a[jj] = make_uint4(a0.x, a0.y, a1.x, a1.y);
     }
+  };
+  auto pv = [&](const uint4 (&a)[VW], const uint4 (&pb)[2]) {
 #pragma unroll
     for (int jj = 0; jj < VW; ++jj) {
       acc[0][jj] = MT::mma_16x16x32(a[jj], pb[0], acc[0][jj]);
       acc[1][jj] = MT::mma_16x16x32(a[jj], pb[1], acc[1][jj]);
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * VW, 0);  // all V^T fragment reads first
-    __builtin_amdgcn_sched_group_barrier(0x008, 2 * VW, 0);  // then the MFMAs
   };
   // Ping-pong: the two wavefronts that share a SIMD (one of waves {0,2,5,7},
   // one of {1,3,4,6}, for either round-robin or paired wave placement) put
@@ -509,8 +544,10 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     __syncthreads();
     f32x4 sc[2][2];
     uint4 pbk[2];
-    // step 0: scores of tile t0; group B also its softmax
+    uint4 va[VW];
+    // step 0: scores and V^T fragments of tile t0; group B also its softmax
     qk(0, sc);
+    vfrag(0, va);
     if (!grp_a) {
       sm_max(t0, sc);
       sm_exp(sc, pbk);
@@ -529,8 +566,9 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
           sm_max(T - 1, sc);
           sm_exp(sc, pbk);
         }
-        pv(u % 3, pbk);            // stage of tile T-1 = (ii-1) % 3 = u
+        pv(va, pbk);               // tile T-1, fragments read in the previous step
         qk((u + 1) % 3, sc);       // stage of tile T = ii % 3
+        vfrag((u + 1) % 3, va);
         if (!grp_a) {
           sm_max(T, sc);
           sm_exp(sc, pbk);
@@ -545,7 +583,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       sm_max(t1 - 1, sc);
       sm_exp(sc, pbk);
     }
-    pv((n - 1) % 3, pbk);
+    pv(va, pbk);
   }
 
   // ---- epilogue: lane holds dims 16*jj + 4*grp + r of its row
@@ -587,7 +625,7 @@ extern "C" int64_t mi_prefill_workspace_bytes(int32_t batch, int32_t max_qo_toke
   using namespace mi;
   if (batch < 0 || max_qo_tokens < 0 || num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads)
     return MI_ERR_INVALID;
-  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, num_qo_heads / num_kv_heads, head_dim);
+  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, num_qo_heads / num_kv_heads, num_kv_heads, head_dim);
   return L.split + split_layout(batch, num_kv_heads, head_dim, -1).total;
 }
 
@@ -606,7 +644,7 @@ extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
   if (page_size % 16 || !ok_head_dim(head_dim)) return MI_ERR_UNSUPPORTED;
   const int G = num_qo_heads / num_kv_heads;
   if (G > kShortRows) return MI_ERR_UNSUPPORTED;
-  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, head_dim);
+  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, num_kv_heads, head_dim);
   if (workspace_bytes < L.split) return MI_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
   uint8_t* ws = (uint8_t*)workspace;
@@ -617,7 +655,7 @@ extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
   hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, qo_indptr, kv_indptr, last_page_len, batch,
                      page_size, G, num_kv_heads, pf_rows(head_dim), L.max_tiles, /*cost model: causal*/ 1,
                      (int32_t*)(ws + L.hdr),
-                     (int2*)(ws + L.tiles), (int32_t*)(ws + L.tcum));
+                     (int2*)(ws + L.tiles), (int32_t*)(ws + L.tcum), (int32_t*)(ws + L.order));
   MI_CHECK_LAUNCH();
   return decode_plan_impl(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
                           num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, L.split, s);
@@ -645,7 +683,7 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
   if (q_dtype != MI_BF16 && q_dtype != MI_F16) return MI_ERR_UNSUPPORTED;
   if (!fp8 && kv->dtype != q_dtype) return MI_ERR_UNSUPPORTED;
   if (fp8 && (!kv->k_scale || !kv->v_scale)) return MI_ERR_INVALID;
-  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, D);
+  const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, nkv, D);
   if (workspace_bytes < L.split) return MI_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
   int st = MI_OK;
@@ -675,6 +713,7 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
   pp.last_page_len = last_page_len;
   pp.hdr = (const int32_t*)(ws + L.hdr);
   pp.tiles = (const int2*)(ws + L.tiles);
+  pp.order = (const int32_t*)(ws + L.order);
   pp.ctr = (int32_t*)((uint8_t*)workspace + L.ctr);
   pp.out = out;
   pp.out_stride_tok = out_stride_token;
