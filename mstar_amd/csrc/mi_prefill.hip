@@ -497,6 +497,8 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // The fragments of tile T are read in the step that computes its scores
   // and kept in registers across the barrier: the P.V MFMAs of the next
   // step then start without waiting on LDS, while that step's K reads run.
+  // head_dim 256 (64 registers of fragments) reads them just before use.
+  constexpr bool VPRE = D <= 128;
   auto vfrag = [&](int stage, uint4 (&a)[VW]) {
     const uint8_t* vt0 = lds + stage * STAGE + KEYS * RSK + (4 * grp + ((lane & 15) >> 2)) * RSV + 8 * (lane & 3);
 #pragma unroll
@@ -547,7 +549,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     uint4 va[VW];
     // step 0: scores and V^T fragments of tile t0; group B also its softmax
     qk(0, sc);
-    vfrag(0, va);
+    if constexpr (VPRE) vfrag(0, va);
     if (!grp_a) {
       sm_max(t0, sc);
       sm_exp(sc, pbk);
@@ -566,9 +568,10 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
           sm_max(T - 1, sc);
           sm_exp(sc, pbk);
         }
-        pv(va, pbk);               // tile T-1, fragments read in the previous step
+        if constexpr (!VPRE) vfrag(u % 3, va);  // stage of tile T-1 = (ii-1) % 3 = u
+        pv(va, pbk);               // tile T-1
         qk((u + 1) % 3, sc);       // stage of tile T = ii % 3
-        vfrag((u + 1) % 3, va);
+        if constexpr (VPRE) vfrag((u + 1) % 3, va);
         if (!grp_a) {
           sm_max(T, sc);
           sm_exp(sc, pbk);
@@ -583,6 +586,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       sm_max(t1 - 1, sc);
       sm_exp(sc, pbk);
     }
+    if constexpr (!VPRE) vfrag((n - 1) % 3, va);
     pv(va, pbk);
   }
 
