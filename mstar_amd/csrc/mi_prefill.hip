@@ -40,8 +40,8 @@ constexpr int kPfKeys = 32;                // keys per K/V tile
 constexpr int kPfPageCap = 2048;           // page ids staged in LDS at a time
 constexpr int kShortRows = 16;  // qo_len * group <= 16 -> decode kernel
 
-// Workspace: header | per-XCD queue counters | tile list | tile cost prefix |
-// unit order | decode split plan.
+// Workspace: header | per-XCD queue counters + finished-workgroup counter |
+// tile list | tile cost prefix | unit order | decode split plan.
 // Header words: [0] tiles, [1] units (tiles x kv-heads), [8 + x] first unit
 // of XCD x's queue (x = 0..8, [16] = units).
 struct PrefillLayout {
@@ -60,7 +60,7 @@ static PrefillLayout prefill_layout(int32_t batch, int32_t max_qo_tokens, int32_
   L.max_tiles = (int32_t)mt;
   L.hdr = 0;
   L.ctr = 256;
-  L.tiles = L.ctr + 8 * kCtrStride * 4;
+  L.tiles = L.ctr + 9 * kCtrStride * 4;
   L.tcum = mi_align_up(L.tiles + 8LL * L.max_tiles, 256);
   L.order = mi_align_up(L.tcum + 4LL * (L.max_tiles + 1), 256);
   L.split = mi_align_up(L.order + 4LL * L.max_tiles * nkv, 256);
@@ -119,10 +119,10 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* qo_in
                                                             int32_t page_size, int32_t group, int32_t nkv,
                                                             int32_t tile_rows, int32_t max_tiles, int32_t causal,
                                                             int32_t* hdr, int2* tiles, int32_t* tcum,
-                                                            int32_t* order) {
+                                                            int32_t* order, int32_t* ctr) {
   __shared__ int smem[16];
   __shared__ int s_cut[9];
-  __shared__ int s_bin[1024];
+  __shared__ int s_bin[8 * 1024];
   int carry = 0, carry_cost = 0;
   for (int base = 0; base < batch; base += 1024) {
     const int b = base + (int)threadIdx.x;
@@ -177,33 +177,38 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* qo_in
     s_cut[x] = (int)u0;
   }
   __syncthreads();
-  // Within each queue, units go heaviest first (counting sort by cost,
-  // clamped to 1023 steps), so the tail of the kernel runs the short ones.
-  for (int x = 0; x < 8; ++x) {
-    const int lo = s_cut[x], hi = s_cut[x + 1];
-    s_bin[threadIdx.x] = 0;
-    __syncthreads();
-    for (int u = lo + (int)threadIdx.x; u < hi; u += 1024) {
-      const int t = u % n_tiles;
-      atomicAdd(&s_bin[1023 - min(tcum[t + 1] - tcum[t], 1023)], 1);
+  // Within each queue, units go heaviest first: one counting sort over
+  // (queue, 1023 - min(cost, 1023)) keys in LDS.  Queues are contiguous unit
+  // ranges, so the sorted positions of queue x start at its first unit.
+  for (int i = threadIdx.x; i < 8 * 1024; i += 1024) s_bin[i] = 0;
+  __syncthreads();
+  auto key_of = [&](int u) {
+    int x = 0;
+#pragma unroll
+    for (int k = 1; k < 8; ++k) x += u >= s_cut[k];
+    const int t = u % n_tiles;
+    return x * 1024 + 1023 - min(tcum[t + 1] - tcum[t], 1023);
+  };
+  for (int u = (int)threadIdx.x; u < (int)units; u += 1024) atomicAdd(&s_bin[key_of(u)], 1);
+  __syncthreads();
+  {
+    int loc[8], sum = 0;  // thread t owns bins [8t, 8t + 8)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      loc[k] = sum;
+      sum += s_bin[8 * threadIdx.x + k];
     }
-    __syncthreads();
     int tot;
-    const int start = block_exclusive_scan_1024(s_bin[threadIdx.x], tot, smem) + lo;
+    const int base = block_exclusive_scan_1024(sum, tot, smem);
     __syncthreads();
-    s_bin[threadIdx.x] = start;
-    __syncthreads();
-    for (int u = lo + (int)threadIdx.x; u < hi; u += 1024) {
-      const int t = u % n_tiles;
-      order[atomicAdd(&s_bin[1023 - min(tcum[t + 1] - tcum[t], 1023)], 1)] = u;
-    }
-    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s_bin[8 * threadIdx.x + k] = base + loc[k];
   }
+  __syncthreads();
+  for (int u = (int)threadIdx.x; u < (int)units; u += 1024) order[atomicAdd(&s_bin[key_of(u)], 1)] = u;
+  if (threadIdx.x < 9) ctr[threadIdx.x * kCtrStride] = 0;  // queues of the first run
 }
 
-__global__ void prefill_reset_kernel(int32_t* ctr) {
-  if (threadIdx.x < 8) ctr[threadIdx.x * kCtrStride] = 0;
-}
 
 // ------------------------------------------------------------ attention
 struct PrefillParams {
@@ -607,6 +612,15 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     }
   }
   }  // unit loop
+  // The last workgroup to finish resets the queues for the next run with
+  // this plan (every other workgroup has taken its last unit by then).
+  if (threadIdx.x == 0) {
+    __threadfence();
+    if (atomicAdd(p.ctr + 8 * kCtrStride, 1) == (int)gridDim.x - 1) {
+#pragma unroll
+      for (int y = 0; y < 9; ++y) __hip_atomic_store(p.ctr + y * kCtrStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 template <typename MT, bool FP8>
@@ -659,7 +673,8 @@ extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
   hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, qo_indptr, kv_indptr, last_page_len, batch,
                      page_size, G, num_kv_heads, pf_rows(head_dim), L.max_tiles, /*cost model: causal*/ 1,
                      (int32_t*)(ws + L.hdr),
-                     (int2*)(ws + L.tiles), (int32_t*)(ws + L.tcum), (int32_t*)(ws + L.order));
+                     (int2*)(ws + L.tiles), (int32_t*)(ws + L.tcum), (int32_t*)(ws + L.order),
+                     (int32_t*)(ws + L.ctr));
   MI_CHECK_LAUNCH();
   return decode_plan_impl(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
                           num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, L.split, s);
@@ -734,7 +749,6 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
     return MI_ERR_LAUNCH;
   const int64_t units = (int64_t)L.max_tiles * nkv;
   const int grid = (int)(((units < ncu ? units : (int64_t)ncu) + 7) / 8 * 8);
-  hipLaunchKernelGGL(prefill_reset_kernel, dim3(1), dim3(64), 0, s, pp.ctr);
   if (q_dtype == MI_BF16)
     st = fp8 ? launch_prefill<BF16, true>(pp, D, grid, s) : launch_prefill<BF16, false>(pp, D, grid, s);
   else
