@@ -334,7 +334,9 @@ def bench_decode(args, dev) -> dict:
             "algorithmic_bytes": int(np.mean(bytes_per)),
         },
     }
-    res["rope"] = bench_rope(q, k, np.array([cm._get_state(r).seq_len for r in rids]), args.steps)
+    pos_now = np.array([cm._get_state(r).seq_len for r in rids])
+    res["rope"] = bench_rope(q, k, pos_now, args.steps)
+    res["rope_append"] = bench_rope_append(cm, q, k, v, pos_now, args.steps)
     res["kv_transfer"] = bench_transfer(kv, args.steps)
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
@@ -342,26 +344,22 @@ def bench_decode(args, dev) -> dict:
     return res
 
 
-def bench_rope(q, k, positions: np.ndarray, steps: int, per_graph: int = 20) -> dict:
-    """apply_rope on this step's q and k (in place, on copies): HBM read + write of both.
+def _graph_us(fn, device, steps: int, per_graph: int = 20) -> float:
+    """Mean time of one ``fn()`` from HIP graph replays of ``per_graph`` captured calls.
 
-    The kernel is shorter than a Python launch, so launches are captured in a
-    HIP graph and replayed; the per-launch time is the replay time / launches.
+    The kernels involved are shorter than a Python launch, so host-issued
+    launches would time the host; replaying a captured graph times the GPU.
     """
-    from mstar_amd.rope import apply_rope_pos_ids_inplace
-
-    qc, kc = q.clone(), k.clone()
-    pos = torch.as_tensor(positions, dtype=torch.int64, device=q.device)
-    side = torch.cuda.Stream(device=q.device)
-    side.wait_stream(torch.cuda.current_stream(q.device))
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(side):
         for _ in range(3):
-            apply_rope_pos_ids_inplace(qc, kc, pos, rope_theta=1e6)
-    torch.cuda.current_stream(q.device).wait_stream(side)
+            fn()
+    torch.cuda.current_stream(device).wait_stream(side)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for _ in range(per_graph):
-            apply_rope_pos_ids_inplace(qc, kc, pos, rope_theta=1e6)
+            fn()
     graph.replay()
     torch.cuda.synchronize()
     evs = _kernel_events(max(steps // 5, 3), 2)
@@ -370,11 +368,53 @@ def bench_rope(q, k, positions: np.ndarray, steps: int, per_graph: int = 20) -> 
         graph.replay()
         e1.record()
     torch.cuda.synchronize()
-    us = float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3 / per_graph
+    return float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3 / per_graph
+
+
+def bench_rope(q, k, positions: np.ndarray, steps: int, per_graph: int = 20) -> dict:
+    """apply_rope on this step's q and k (in place, on copies): HBM read + write of both."""
+    from mstar_amd.rope import apply_rope_pos_ids_inplace
+
+    qc, kc = q.clone(), k.clone()
+    pos = torch.as_tensor(positions, dtype=torch.int64, device=q.device)
+    us = _graph_us(lambda: apply_rope_pos_ids_inplace(qc, kc, pos, rope_theta=1e6), q.device, steps, per_graph)
     nbytes = 2 * (qc.numel() + kc.numel()) * qc.element_size() + pos.numel() * 8
     return {"kernel": "rope_kernel", "what": "apply_rope_pos_ids_inplace on the step's q [B, Hq, D] and k [B, Hkv, D], "
             f"{per_graph} launches per HIP graph replay", "kernel_us": us, "algorithmic_bytes": nbytes,
             "GBps": nbytes / (us * 1e-6) / 1e9}
+
+
+def bench_rope_append(cm, q, k, v, positions: np.ndarray, steps: int, per_graph: int = 20) -> dict:
+    """One layer's RoPE + K/V append: two launches (rope_kernel, append_kernel) vs rope_append_kernel.
+
+    Both write this step's slots of layer 0 (the decode wrapper's planned
+    locations); q and k are copies rotated in place.
+    """
+    from mstar_amd.rope import apply_rope_pos_ids_inplace
+
+    w = cm._plan_states["main"].wrapper
+    layer = cm.kv_cache[0]
+    ks, vs = _layer_scales(cm)
+    qc, kc = q.clone(), k.clone()
+    pos = torch.as_tensor(positions, dtype=torch.int64, device=q.device)
+
+    def two():
+        apply_rope_pos_ids_inplace(qc, kc, pos, rope_theta=1e6)
+        w.set_kv_cache(layer, kc, v, k_scale=ks, v_scale=vs)
+
+    def one():
+        w.rope_set_kv_cache(layer, qc, kc, v, pos, rope_theta=1e6, k_scale=ks, v_scale=vs)
+
+    t_two = _graph_us(two, q.device, steps, per_graph)
+    t_one = _graph_us(one, q.device, steps, per_graph)
+    kv_elem = layer.element_size()
+    # fused: read q, k, v and positions, write q, k and the cache's K and V rows
+    nbytes = (2 * q.numel() + 2 * k.numel() + v.numel()) * q.element_size() + pos.numel() * 8 \
+        + 2 * k.numel() * kv_elem + 16 * q.shape[0]
+    return {"kernel": "rope_append_kernel", "what": "decode wrapper rope_set_kv_cache vs apply_rope_pos_ids_inplace + "
+            f"set_kv_cache on the step's q, k, v, {per_graph} per HIP graph replay",
+            "two_launches_us": t_two, "fused_us": t_one, "algorithmic_bytes": nbytes,
+            "GBps": nbytes / (t_one * 1e-6) / 1e9}
 
 
 def bench_transfer(kv_layer: torch.Tensor, steps: int, pages: int = 32768, host_pages: int = 4096) -> dict:

@@ -249,6 +249,26 @@ int mi_rope_apply(void* q, int64_t q_stride_token, int64_t q_stride_head, int32_
                   int32_t num_tokens, int32_t interleave, float rope_scale, float rope_theta,
                   int32_t llama31, float low_freq_factor, float high_freq_factor, float old_context_len,
                   void* stream);
+/* mi_rope_append fuses BatchedCacheManager.apply_rope (cache_manager.py:702-760)
+ * with the K/V append of run_attention (cache_manager.py:653-701 ->
+ * FlashInfer*Wrapper.set_kv_cache, flashinfer_utils.py:271-288, 467-484):
+ * one pass that rotates q in place (as mi_rope_apply), rotates k (in place
+ * when keep_k != 0), and writes the rotated k and v [num_tokens,
+ * kv->num_kv_heads, kv->head_dim] of tokens t < min(num_append_tokens,
+ * *num_tokens_device) to their cache slots (as mi_kv_append with num_tokens =
+ * num_append_tokens, and the same page_idx/slot_idx/idx_stride meaning; k and
+ * v in `dtype`, 16-byte aligned rows).  All num_tokens tokens of q and k are
+ * rotated.  The cache contents, q and (with keep_k) k are bit-identical to
+ * mi_rope_apply followed by mi_kv_append.
+ * ------------------------------------------------------------------------ */
+int mi_rope_append(void* q, int64_t q_stride_token, int64_t q_stride_head, int32_t num_qo_heads, void* k,
+                   int64_t k_stride_token, int64_t k_stride_head, const void* v, int64_t v_stride_token,
+                   int64_t v_stride_head, int32_t dtype, int32_t keep_k, const mi_paged_kv* kv,
+                   const int64_t* page_idx, const int64_t* slot_idx, int64_t idx_stride,
+                   int32_t num_append_tokens, const int32_t* num_tokens_device, int32_t rotary_dim,
+                   const void* pos_ids, int32_t pos_dtype, int32_t num_tokens, int32_t interleave,
+                   float rope_scale, float rope_theta, int32_t llama31, float low_freq_factor,
+                   float high_freq_factor, float old_context_len, void* stream);
 
 /* ------------------------------------------------------------------------
  * Page snapshot copies (multi-label / CFG planning).

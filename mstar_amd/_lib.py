@@ -142,6 +142,11 @@ SIGNATURES = {
         [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _I32, _I32, _I32, _F32, _F32,
          _I32, _F32, _F32, _F32, _P],
     ),
+    "mi_rope_append": (
+        ctypes.c_int,
+        [_P, _I64, _I64, _I32, _P, _I64, _I64, _P, _I64, _I64, _I32, _I32, ctypes.POINTER(MiPagedKV), _P, _P,
+         _I64, _I32, _P, _I32, _P, _I32, _I32, _I32, _F32, _F32, _I32, _F32, _F32, _F32, _P],
+    ),
 }
 
 _lock = threading.Lock()

@@ -6,7 +6,9 @@ BatchedCacheManager`` (``cache_manager.py:56-881``): ``plan_attention``,
 ``plan_rope_batched_cfg``, ``snapshot_all``, ``set_layer_idx``, ``set_active_label(s)``,
 ``get_qo_indptr_buf``, ``advance_seq_len(s)``, ``set_custom_pos_advance``,
 ``flush_to_store``, plus the pre-planned-label fast path used by the CUDA-graph
-runner (``_pre_planned_labels``, ``cache_manager.py:202-217``).
+runner (``_pre_planned_labels``, ``cache_manager.py:202-217``).  One method has
+no reference counterpart: ``apply_rope_and_run_attention`` fuses the RoPE of
+``apply_rope`` with the K/V append of ``run_attention`` into one kernel.
 
 What changes is how a step is packed (``_plan_attention_impl``,
 ``cache_manager.py:229-424``).  The reference walks every request in Python,
@@ -457,6 +459,47 @@ class BatchedCacheManager:
             apply_rope_pos_ids_inplace(q, k, ps.pos_ids, rotary_dim=rotary_dim, interleave=interleave,
                                        rope_scale=rope_scale, rope_theta=rope_theta)
         return q.to(orig_dtype), k.to(orig_dtype)
+
+    def apply_rope_and_run_attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                                     rotary_dim: int | None = None, interleave: bool = False, rope_scale: float = 1,
+                                     rope_theta: float = 10000.0, rope_dtype=None, layer_idx: int | None = None,
+                                     keep_k: bool = True, **kwargs) -> torch.Tensor:
+        """``apply_rope(q, k, ...)`` then ``run_attention(q, k, v)`` with the rotation and the append fused.
+
+        One ``mi_rope_append`` launch rotates q (and k, unless ``keep_k`` is
+        False) and writes the rotated k and v to the layer's pages; the cache
+        and the attention output are bit-identical to the two-call sequence.
+        Dtype handling and Llama-3.1 keywords are those of ``apply_rope``; v
+        is converted to the rope dtype with q and k.
+        """
+        if layer_idx is None:
+            layer_idx = self.layer_idx
+        label = self._single_active_label()
+        ps = self._plan_states[label]
+        assert ps.pos_ids is not None, "plan_rope() must run before apply_rope_and_run_attention()"
+        assert self.kv_cache is not None and ps.wrapper is not None
+        orig_dtype = q.dtype
+        dt = rope_dtype
+        if dt is None and torch.is_autocast_enabled("cuda"):
+            dt = torch.get_autocast_dtype("cuda")
+        if dt is None and q.dtype == torch.float32:
+            dt = torch.bfloat16
+        if dt is not None:
+            q, k, v = q.to(dt), k.to(dt), v.to(dt)
+        elif v.dtype != k.dtype:
+            v = v.to(k.dtype)
+        llama31 = {key: val for key, val in kwargs.items() if key in _LLAMA31_KEYS and val is not None}
+        if llama31:  # apply_llama31_rope_pos_ids_inplace defaults for the factors not given
+            llama31 = {"low_freq_factor": 1.0, "high_freq_factor": 4.0, "old_context_len": 8192, **llama31}
+        layer = self.kv_cache[layer_idx]
+        ks, vs = self._layer_scales(layer_idx)
+        ps.wrapper.rope_set_kv_cache(layer, q, k, v, ps.pos_ids, rotary_dim=rotary_dim, interleave=interleave,
+                                     rope_scale=rope_scale, rope_theta=rope_theta, k_scale=ks, v_scale=vs,
+                                     keep_k=keep_k, llama31=llama31 or None)
+        if self.auto_write_store and ps.write_store:
+            for rid in self.request_ids:
+                self.alloc_manager.flush_to_store(rid, label=label, layers=layer_idx)
+        return ps.wrapper.run(q, layer, ks, vs).to(orig_dtype)
 
     # ------------------------------------------------------------ advance
     def advance_seq_len(self, n: int | None = None, pos_id_n: int | None = None) -> None:

@@ -21,6 +21,8 @@ Differences from the reference, all deliberate:
   page 0 slot 0, ``flashinfer_utils.py:251-253``).
 * Optional fp8-e4m3 KV caches (``torch.float8_e4m3fn``) with per-head fp32
   ``k_scale``/``v_scale`` passed to ``set_kv_cache`` and ``run``.
+* ``rope_set_kv_cache`` (no reference counterpart) fuses the RoPE call that
+  precedes ``set_kv_cache`` in every layer with the append itself.
 """
 
 from __future__ import annotations
@@ -148,7 +150,36 @@ def _append(kv_cache_layer: torch.Tensor, k: torch.Tensor, v: torch.Tensor, page
     )
 
 
-class PagedDecodeWrapper:
+def _rope_set_kv_cache(wrapper, kv_cache_layer, q, k, v, pos_ids, rotary_dim, interleave, rope_scale, rope_theta,
+                       k_scale, v_scale, keep_k, llama31) -> None:
+    from .rope import rope_append
+
+    page_idx, slot_ptr, idx_stride, n, n_dev = wrapper._append_target()
+    rope_append(q, k, v, kv_cache_layer, pos_ids, page_idx, slot_ptr, idx_stride, n, n_dev,
+                rotary_dim=rotary_dim, interleave=interleave, rope_scale=rope_scale, rope_theta=rope_theta,
+                k_scale=k_scale, v_scale=v_scale, keep_k=keep_k, llama31=llama31)
+
+
+class _FusedRopeAppend:
+    """``rope_set_kv_cache``: RoPE on q/k fused with ``set_kv_cache`` (one launch)."""
+
+    def rope_set_kv_cache(self, kv_cache_layer: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          pos_ids: torch.Tensor, rotary_dim: int | None = None, interleave: bool = False,
+                          rope_scale: float = 1, rope_theta: float = 1e4, k_scale: torch.Tensor | None = None,
+                          v_scale: torch.Tensor | None = None, keep_k: bool = True,
+                          llama31: dict | None = None) -> None:
+        """``apply_rope_pos_ids_inplace(q, k, pos_ids, ...)`` then ``set_kv_cache(kv_cache_layer, k, v)``.
+
+        Same results bit for bit, in one kernel (``mi_rope_append``).  ``llama31``
+        holds ``low_freq_factor``/``high_freq_factor``/``old_context_len`` for
+        the Llama-3.1 frequencies.  q, k and v share one dtype (bf16 or fp16);
+        k and v rows must be 16-byte aligned.
+        """
+        _rope_set_kv_cache(self, kv_cache_layer, q, k, v, pos_ids, rotary_dim, interleave, rope_scale, rope_theta,
+                           k_scale, v_scale, keep_k, llama31)
+
+
+class PagedDecodeWrapper(_FusedRopeAppend):
     """Batched paged decode attention (``flashinfer_utils.py:291-484``)."""
 
     def __init__(
@@ -284,12 +315,15 @@ class PagedDecodeWrapper:
     def set_kv_cache(self, kv_cache_layer: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None) -> None:
         """Write one new token per request (``flashinfer_utils.py:467-484``)."""
-        n = self._n_req
+        _append(kv_cache_layer, k, v, *self._append_target(), k_scale, v_scale)
+
+    def _append_target(self):
+        """(page ids, slot ids pointer, index stride, tokens, device token count) of this step's append."""
         loc = self.kv_cache_locations
-        _append(kv_cache_layer, k, v, loc, loc.data_ptr() + 8, 2, n, None, k_scale, v_scale)
+        return loc, loc.data_ptr() + 8, 2, self._n_req, None
 
 
-class PagedPrefillWrapper:
+class PagedPrefillWrapper(_FusedRopeAppend):
     """Batched ragged paged prefill attention (``flashinfer_utils.py:70-288``)."""
 
     def __init__(
@@ -458,10 +492,12 @@ class PagedPrefillWrapper:
     def set_kv_cache(self, kv_cache_layer: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None) -> None:
         """Scatter the planned tokens' K/V into their pages (``flashinfer_utils.py:271-288``)."""
-        n = self._total_tokens
+        _append(kv_cache_layer, k, v, *self._append_target(), k_scale, v_scale)
+
+    def _append_target(self):
+        """(page ids, slot ids pointer, index stride, tokens, device token count) of this step's append."""
         n_dev = self._qo.data_ptr() + 4 * self._n_req  # qo_indptr[n_req]: real count on the device
-        _append(kv_cache_layer, k, v, self.token_to_page, self.token_to_cache.data_ptr(), 1, n, n_dev,
-                k_scale, v_scale)
+        return self.token_to_page, self.token_to_cache.data_ptr(), 1, self._total_tokens, n_dev
 
 
 # Reference names (mstar/utils/flashinfer_utils.py) for drop-in use.

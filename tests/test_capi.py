@@ -110,6 +110,37 @@ def test_rope_arguments_are_checked(L):
     assert L.mi_rope_positions(None, None, 0, None, 0, None) == 0
 
 
+def test_rope_append_arguments_are_checked(L):
+    buf = (ctypes.c_int32 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+
+    def kv(**kw):
+        d = _lib.MiPagedKV()
+        d.data, d.dtype, d.page_size, d.num_kv_heads, d.head_dim = 4096, 0, 16, 2, 128
+        d.max_pages, d.page_stride, d.kv_stride, d.token_stride, d.head_stride = 8, 8192, 4096, 256, 128
+        for k, v in kw.items():
+            setattr(d, k, v)
+        return ctypes.byref(d)
+
+    def call(desc, rd=128, dtype=0, k_stride=256, scale=1.0, llama=(0, 1.0, 4.0), ntok=3, nappend=3, pos=p):
+        return L.mi_rope_append(p, 512, 128, 4, p, k_stride, 128, p, 256, 128, dtype, 1, desc, p, p, 1, nappend,
+                                None, rd, pos, 5, ntok, 0, scale, 1e4, llama[0], llama[1], llama[2], 8192.0, None)
+
+    assert call(kv(), ntok=0) == 0                                      # nothing to do
+    assert call(kv(), nappend=-1) == MI_ERR_INVALID
+    assert call(None) == MI_ERR_INVALID
+    assert call(kv(), pos=None) == MI_ERR_INVALID
+    assert call(kv(), rd=12) == MI_ERR_UNSUPPORTED                      # rotary_dim % 8
+    assert call(kv(), rd=256) == MI_ERR_UNSUPPORTED                     # rotary_dim > head_dim
+    assert call(kv(), dtype=2) == MI_ERR_UNSUPPORTED                    # fp32 q/k/v
+    assert call(kv(dtype=3)) == MI_ERR_INVALID                          # fp8 cache without scales
+    assert call(kv(), scale=0.0) == MI_ERR_INVALID
+    assert call(kv(), llama=(1, 4.0, 1.0)) == MI_ERR_INVALID            # high <= low
+    assert call(kv(), k_stride=260) == MI_ERR_INVALID                   # k rows not 8-element aligned
+    assert call(kv(token_stride=260)) == MI_ERR_INVALID                 # cache rows not 8-element aligned
+    assert call(kv(data=4100)) == MI_ERR_INVALID                        # cache base not 16-byte aligned
+
+
 def test_transfer_arguments_are_checked(L):
     """KV transfer: malformed pool descriptors and ranges fail before any HIP call."""
     buf = (ctypes.c_int32 * 64)()
