@@ -122,6 +122,7 @@ class BatchedCacheManager:
         self._pre_planned_labels: set[str] = set()
         self._plan_done_event = None
         self._pack = _PackBuffers(self.device)
+        self._states_cache: dict = {}
         if alloc_manager.block_table is None:
             raise ValueError("the allocation manager needs a device (block table) for GPU packing")
 
@@ -164,7 +165,7 @@ class BatchedCacheManager:
             return
         self._plan_attention_impl(seq_lens, dtype, is_causal, write_store, effective)
 
-    def _alloc_entries(self, entries: list[tuple[str, str]], seq_lens) -> np.ndarray:
+    def _alloc_entries(self, entries: list[tuple[str, str]], seq_lens, states=None) -> np.ndarray:
         """FIFO allocation in batch order (``cache_manager.py:278-285``) and the pack
         kernel's input: per entry ``[slot | seq_len | new_len | num_pages | pages
         already on the device]``, followed by the pages not yet on the device.
@@ -173,20 +174,32 @@ class BatchedCacheManager:
         n = len(entries)
         if len(seq_lens) != n:
             raise ValueError(f"{len(seq_lens)} seq_lens for {n} requests")
-        states = []
+        if states is None:
+            states = [self._get_state(rid, label) for rid, label in entries]
+        seq = np.fromiter((st.seq_len for st in states), dtype=np.int64, count=n)
+        sl = np.asarray(seq_lens, dtype=np.int64).reshape(n)
+        self.alloc_manager.alloc_batch(entries, states, seq + sl)
+        slots, npg, old, new_pages = self.alloc_manager.block_table.prepare_meta(states)
         meta = np.empty((5, n), dtype=np.int32)
-        for i, (rid, label) in enumerate(entries):
-            st = self._get_state(rid, label)
-            sl = int(seq_lens[i])
-            self.alloc_manager.alloc(rid, label=label, seq_len=st.seq_len + sl)
-            states.append(st)
-            meta[1, i] = st.seq_len
-            meta[2, i] = sl
-            meta[3, i] = len(st.page_indices)
-        old, new_pages = self.alloc_manager.block_table.prepare(states)
-        meta[0] = [st.slot for st in states]
+        meta[0] = slots
+        meta[1] = seq
+        meta[2] = sl
+        meta[3] = npg
         meta[4] = old
         return np.concatenate([meta.reshape(-1), new_pages])
+
+    def _label_states(self, label: str) -> tuple[list[tuple[str, str]], list[KVRequestState]]:
+        """Entries ``(rid, label)`` of every request and their state objects, kept
+        while the request list and the allocation manager's states are unchanged."""
+        am = self.alloc_manager
+        key = tuple(self.request_ids)
+        c = self._states_cache.get(label)
+        if c is not None and c[0] == am.state_generation and c[1] == key:
+            return c[2], c[3]
+        entries = [(rid, label) for rid in key]
+        states = [am.get_state(rid, label) for rid in key]
+        self._states_cache[label] = (am.state_generation, key, entries, states)
+        return entries, states
 
     def _launch_pack(self, meta: np.ndarray, qo, kv_indptr, kv_indices, last, loc) -> None:
         """One upload of the step's metadata + new pages, one pack kernel."""
@@ -213,9 +226,11 @@ class BatchedCacheManager:
         cfg = self.kv_cache_config
         ps_ = cfg.page_size
         b = len(self.request_ids)
-        meta = self._alloc_entries([(rid, label) for rid in self.request_ids], seq_lens)
+        entries, states = self._label_states(label)
+        meta = self._alloc_entries(entries, seq_lens, states)
         total_pages = int(meta[3 * b:4 * b].sum())
-        is_decode = all(int(s) == 1 for s in seq_lens)
+        new_lens = meta[2 * b:3 * b]
+        is_decode = bool((new_lens == 1).all())
 
         ps = self._plan_states.get(label)
         if ps is not None and ps.wrapper is not None:
@@ -523,6 +538,18 @@ class BatchedCacheManager:
 
     def advance_seq_lens(self, pos_id_ns: list[int] | int | None = None) -> None:
         """``seq_len += seq_lens[i]`` per request (``cache_manager.py:811-838``)."""
+        labels = set(self.active_labels[rid] for rid in self.request_ids)
+        if len(labels) == 1 and pos_id_ns is None:  # one label, default advance: one pass over the states
+            label = labels.pop()
+            ps = self._plan_states[label]
+            _, states = self._label_states(label)
+            adv = ps.custom_pos_advance if ps.custom_pos_advance is not None else ps.seq_lens
+            for st, n, a in zip(states, ps.seq_lens, adv):
+                st.seq_len += n
+                st.position_id_start += a
+            for ps in self._plan_states.values():
+                ps.custom_pos_advance = None
+            return
         for i, rid in enumerate(self.request_ids):
             ps = self._plan_states[self.active_labels[rid]]
             n = ps.seq_lens[i]

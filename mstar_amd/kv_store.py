@@ -204,6 +204,33 @@ class DeviceBlockTable:
         new = np.fromiter((p for part in parts for p in part), dtype=np.int32) if parts else np.zeros(0, np.int32)
         return old, new
 
+    def prepare_meta(self, states: list[KVRequestState]):
+        """:meth:`prepare` plus each state's slot and page count:
+        ``(slots, num_pages, old, new)``, int32 arrays."""
+        slots, npg, old, parts = [], [], [], []
+        stride = self.stride
+        for st in states:
+            if st.slot < 0:
+                self.acquire(st)
+            pl = st.page_indices
+            n = len(pl)
+            if st._dev_list is pl and n == st._dev_len:  # nothing new (most requests of a decode step)
+                start = n
+            else:
+                if n > stride:
+                    raise ValueError(f"request holds {n} pages, block table rows hold {stride}")
+                start = st._dev_len if (st._dev_list is pl and n >= st._dev_len) else 0
+                if n > start:
+                    parts.append(pl[start:])
+                st._dev_list = pl
+                st._dev_len = n
+            slots.append(st.slot)
+            npg.append(n)
+            old.append(start)
+        new = np.fromiter((p for part in parts for p in part), dtype=np.int32) if parts else np.zeros(0, np.int32)
+        return (np.array(slots, dtype=np.int32), np.array(npg, dtype=np.int32), np.array(old, dtype=np.int32),
+                new)
+
     def sync(self, states: list[KVRequestState], stream: torch.cuda.Stream | None = None) -> None:
         """Bring the device rows of ``states`` up to date (async on ``stream``)."""
         slots, poss, pages = [], [], []
@@ -268,6 +295,9 @@ class PagedAllocationManager:
         self.kv_cache = kv_cache
         self.pending_reads: dict[str, dict[str, list]] = {}
         self._lock = threading.RLock()
+        # Bumped whenever a state object is created or a request removed, so
+        # callers can keep lists of state objects between steps.
+        self.state_generation = 0
         if device is None and kv_cache is not None and kv_cache.is_cuda:
             device = kv_cache.device
         self.block_table: DeviceBlockTable | None = None
@@ -288,6 +318,7 @@ class PagedAllocationManager:
         return
 
     def _new_state(self) -> KVRequestState:
+        self.state_generation += 1
         return KVRequestState()
 
     def get_state(self, request_id: str, label: str) -> KVRequestState:
@@ -314,6 +345,35 @@ class PagedAllocationManager:
                         ),
                     )
                 state.page_indices.extend(new_pages)
+
+    def alloc_batch(self, entries: list[tuple[str, str]], states: list[KVRequestState],
+                    seq_lens_after: np.ndarray) -> None:
+        """``alloc(rid, label, seq_lens_after[i])`` for every entry, in order.
+
+        ``states[i]`` is the state of ``entries[i]``.  When the free list holds
+        every page the batch needs, the pages are taken in one pass and handed
+        out in entry order, which is what the sequential calls would give;
+        otherwise the entries are allocated one by one, so the first one that
+        does not fit raises ``AllocationFailedError`` with the earlier ones
+        holding their pages, as in the reference.
+        """
+        ps = self.config.page_size
+        with self._lock:
+            npg = np.fromiter((len(st.page_indices) for st in states), dtype=np.int64, count=len(states))
+            need = (np.asarray(seq_lens_after, dtype=np.int64) + ps - 1) // ps - npg
+            idx = np.flatnonzero(need > 0).tolist()
+            if not idx:
+                return
+            pages = self.page_allocator.try_allocate(int(need[idx].sum()))
+            if pages is None:
+                for i in idx:
+                    self.alloc(entries[i][0], entries[i][1], int(seq_lens_after[i]))
+                return
+            off = 0
+            for i in idx:
+                k = int(need[i])
+                states[i].page_indices.extend(pages[off:off + k])
+                off += k
 
     def get_labels(self, request_id: str) -> list[str]:
         return list(self.request_states[request_id].keys())
@@ -345,6 +405,7 @@ class PagedAllocationManager:
                     self.block_table.release(state)
             del self.request_states[request_id]
             del self.pending_reads[request_id]
+            self.state_generation += 1
 
     # ----- remote reads (kv_store.py:484-581) -----
 
