@@ -187,9 +187,67 @@ def check(status: int, what: str) -> None:
         raise RuntimeError(f"{what}: {text} (status {status})")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device | None = None) -> int:
     """Raw hipStream_t of torch's current stream on ``device``."""
+    if _raw_stream is not None and isinstance(device, torch.device) and device.index is not None:
+        return _raw_stream(device.index)  # same value, without building a Stream object
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_memcpy_async = None
+
+
+def memcpy_h2d_async(dst: int, src: int, nbytes: int, stream: int) -> None:
+    """hipMemcpyAsync host -> device on ``stream`` (HIP runtime this library is bound to)."""
+    global _memcpy_async
+    if _memcpy_async is None:
+        fn = lib().hipMemcpyAsync  # resolved through the library's own HIP runtime dependency
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+        _memcpy_async = fn
+    rc = _memcpy_async(dst, src, nbytes, 1, stream)  # 1 = hipMemcpyHostToDevice
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpyAsync failed with HIP error {rc}")
+
+
+class PinnedUploader:
+    """Small int32 host arrays to the device through two pinned staging buffers.
+
+    Buffers alternate, so writing this call's data waits only for the copy
+    issued two calls ago; the copy is one hipMemcpyAsync on the current
+    stream into a fresh device tensor.
+    """
+
+    def __init__(self, device: torch.device):
+        self.device = torch.device(device)
+        self._bufs: list = [None, None]
+        self._events: list = [None, None]
+        self._i = 0
+
+    def upload(self, arr) -> torch.Tensor:
+        n = int(arr.size)
+        i = self._i
+        self._i ^= 1
+        buf = self._bufs[i]
+        if buf is None or buf[1].size < n:
+            t = torch.empty(max(n, 4096), dtype=torch.int32, pin_memory=True)
+            buf = self._bufs[i] = (t, t.numpy())
+            self._events[i] = None
+        ev = self._events[i]
+        if ev is not None:
+            ev.synchronize()  # the copy that last read this buffer is done
+        buf[1][:n] = arr
+        dev = torch.empty(max(n, 1), dtype=torch.int32, device=self.device)
+        stream = stream_ptr(self.device)
+        if n:
+            memcpy_h2d_async(dev.data_ptr(), buf[0].data_ptr(), 4 * n, stream)
+        if ev is None:
+            ev = self._events[i] = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.device))
+        return dev[:n]
 
 
 def paged_kv_desc(kv_cache_layer: torch.Tensor, k_scale: torch.Tensor | None = None,

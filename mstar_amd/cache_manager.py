@@ -61,30 +61,24 @@ class WorkspaceBufferManager:
         return self.buffers[label]
 
 
-class _PackBuffers:
-    """Device outputs of mi_pack, reused across steps while they are large enough."""
+def _step_tensors(b: int, total_pages: int, decode: bool, device):
+    """Fresh device outputs of one pack (qo_indptr, kv_indptr, kv_indices,
+    last_page_len and, for decode steps, the int64 write locations), carved
+    from one allocation at 256-byte aligned offsets."""
+    al = lambda x: (x + 63) // 64 * 64  # int32 elements per 256 bytes
+    n_loc = al(4 * b) if decode else 0
+    o_qo = n_loc
+    o_ip = o_qo + al(b + 1)
+    o_last = o_ip + al(b + 1)
+    o_idx = o_last + al(b)
+    buf = torch.empty(o_idx + max(total_pages, 1), dtype=torch.int32, device=device)
+    loc = buf[: 4 * b].view(torch.int64).view(b, 2) if decode else None
+    return (buf[o_qo:o_qo + b + 1], buf[o_ip:o_ip + b + 1], buf[o_idx:o_idx + max(total_pages, 1)],
+            buf[o_last:o_last + b], loc)
 
-    def __init__(self, device):
-        self.device = device
-        self.meta: torch.Tensor | None = None
-        self.indices: torch.Tensor | None = None
-        self.locations: torch.Tensor | None = None
-        self.staging: torch.Tensor | None = None
-        self.event: torch.cuda.Event | None = None
 
-    def upload(self, arr: np.ndarray) -> torch.Tensor:
-        n = arr.size
-        if self.staging is None or self.staging.numel() < n:
-            self.staging = torch.empty(max(n, 4096), dtype=torch.int32, pin_memory=True)
-            self.event = None
-        if self.event is not None:
-            self.event.synchronize()
-        self.staging[:n].numpy()[:] = arr
-        dev = torch.empty(n, dtype=torch.int32, device=self.device)
-        dev.copy_(self.staging[:n], non_blocking=True)
-        self.event = torch.cuda.Event()
-        self.event.record()
-        return dev
+class _PackBuffers(_lib.PinnedUploader):
+    """Uploads of the step metadata (one pinned staging pair per manager)."""
 
 
 class BatchedCacheManager:
@@ -259,12 +253,9 @@ class BatchedCacheManager:
             last = wrapper._paged_kv_last_page_len_buf
             if total_pages > kv_indices.shape[0]:
                 raise ValueError(f"{total_pages} pages > wrapper max_num_pages {kv_indices.shape[0]}")
+            loc = torch.empty(b, 2, dtype=torch.long, device=self.device) if is_decode else None
         else:
-            qo = torch.empty(b + 1, dtype=torch.int32, device=self.device)
-            kv_indptr = torch.empty(b + 1, dtype=torch.int32, device=self.device)
-            kv_indices = torch.empty(max(total_pages, 1), dtype=torch.int32, device=self.device)
-            last = torch.empty(b, dtype=torch.int32, device=self.device)
-        loc = torch.empty(b, 2, dtype=torch.long, device=self.device) if is_decode else None
+            qo, kv_indptr, kv_indices, last, loc = _step_tensors(b, total_pages, is_decode, self.device)
         self._launch_pack(meta, qo, kv_indptr, kv_indices, last, loc)
         self._last_pack = (qo, kv_indptr, kv_indices[:total_pages], last, loc)
         if isinstance(wrapper, PagedDecodeWrapper):
