@@ -411,6 +411,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   constexpr float kLazy = 8.f;
   const float lazy_raw = kLazy / sl2;
   float m_run[2] = {kNegInf, kNegInf}, l_run[2] = {0.f, 0.f};
+  float thr[2] = {kNegInf, kNegInf};  // m_run + lazy_raw
 
   // first tile that reaches past some row's limit: (t+1)*KEYS > mask_from
   const int t_mask = mask_from > 0 ? mask_from / KEYS : 0;
@@ -457,8 +458,10 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
           for (int r = 0; r < 4; ++r)
             if (kb + 16 * js + 4 * grp + r > lim[rg]) s[rg][js][r] = kNegInf;
     }
-    float mt[2];
-    bool grow[2];
+    // A row's max exceeds the threshold iff one of its four lanes' maxima
+    // does, so the cross-lane row max is only needed on the rare branch.
+    float ml[2];
+    bool need[2];
 #pragma unroll
     for (int rg = 0; rg < 2; ++rg) {
       float m = kNegInf;
@@ -466,14 +469,19 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       for (int js = 0; js < 2; ++js)
 #pragma unroll
         for (int r = 0; r < 4; ++r) m = fmaxf(m, s[rg][js][r]);
-      mt[rg] = rows4_max(m);
-      grow[rg] = mt[rg] > m_run[rg] + lazy_raw;
+      ml[rg] = m;
+      need[rg] = m > thr[rg];
     }
-    if (__builtin_amdgcn_ballot_w64(grow[0] || grow[1])) {
+    if (__builtin_amdgcn_ballot_w64(need[0] || need[1])) {
 #pragma unroll
       for (int rg = 0; rg < 2; ++rg) {
-        const float alpha = grow[rg] ? fast_exp2((m_run[rg] - mt[rg]) * sl2) : 1.f;
-        if (grow[rg]) m_run[rg] = mt[rg];
+        const float mt = rows4_max(ml[rg]);
+        const bool grow = mt > thr[rg];
+        const float alpha = grow ? fast_exp2((m_run[rg] - mt) * sl2) : 1.f;
+        if (grow) {
+          m_run[rg] = mt;
+          thr[rg] = mt + lazy_raw;
+        }
         l_run[rg] *= alpha;
 #pragma unroll
         for (int jj = 0; jj < VW; ++jj) acc[rg][jj] *= alpha;
