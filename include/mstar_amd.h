@@ -92,6 +92,22 @@ int mi_pack(const int32_t* req_slot, const int32_t* seq_len, const int32_t* new_
             int32_t page_size, int32_t* qo_indptr, int32_t* kv_indptr, int32_t* kv_indices,
             int32_t* last_page_len, int64_t* kv_locations, int32_t grid_blocks, void* stream);
 
+/* mi_pack followed by mi_decode_plan(NULL, kv_indptr, kv_indices, last_page_len, batch,
+ * page_size, num_qo_heads, num_kv_heads, head_dim, NULL, workspace, workspace_bytes) in
+ * one launch, for decode steps (new_len[r] == 1 for every request; kv_locations as in
+ * mi_pack).  The plan workgroup reads the per-request page counts num_pages directly, so
+ * it runs beside the packing workgroups; the packed arrays and the plan in the workspace
+ * are those of the two separate calls.  Replaces the pair of calls BatchedCacheManager
+ * makes per decode step (cache_manager.py:399-415 -> FlashInferDecodeWrapper.plan,
+ * flashinfer_utils.py:369-453). */
+int mi_pack_plan(const int32_t* req_slot, const int32_t* seq_len, const int32_t* new_len,
+                 const int32_t* num_pages, int32_t batch, int32_t* block_table,
+                 int64_t block_table_stride, const int32_t* table_pages, const int32_t* new_pages,
+                 int32_t page_size, int32_t* qo_indptr, int32_t* kv_indptr, int32_t* kv_indices,
+                 int32_t* last_page_len, int64_t* kv_locations, int32_t grid_blocks,
+                 int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, void* workspace,
+                 int64_t workspace_bytes, void* stream);
+
 /* Incremental device block-table update: block_table[slot[i]*stride + pos[i]] = page[i]
  * for i < n.  Keeps the device copy of each request's page list in step with the
  * host allocator (mstar/engine/kv_store.py:463-482) without re-sending whole lists. */

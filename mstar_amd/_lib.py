@@ -81,6 +81,10 @@ SIGNATURES = {
     "mi_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "mi_abi_version": (ctypes.c_int, []),
     "mi_pack": (ctypes.c_int, [_P, _P, _P, _P, _I32, _P, _I64, _P, _P, _I32, _P, _P, _P, _P, _P, _I32, _P]),
+    "mi_pack_plan": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _I32, _P, _I64, _P, _P, _I32, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _I64, _P],
+    ),
     "mi_block_table_update": (ctypes.c_int, [_P, _I64, _P, _P, _P, _I32, _P]),
     "mi_decode_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32]),
     "mi_decode_plan": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _I64, _P]),

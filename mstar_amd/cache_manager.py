@@ -195,22 +195,28 @@ class BatchedCacheManager:
         self._states_cache[label] = (am.state_generation, key, entries, states)
         return entries, states
 
-    def _launch_pack(self, meta: np.ndarray, qo, kv_indptr, kv_indices, last, loc) -> None:
-        """One upload of the step's metadata + new pages, one pack kernel."""
+    def _launch_pack(self, meta: np.ndarray, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=None) -> None:
+        """One upload of the step's metadata + new pages, one pack kernel; with
+        ``plan_wrapper`` (a decode wrapper, decode step) the same launch also
+        writes that wrapper's split-KV plan (``mi_pack_plan``)."""
         b = qo.shape[0] - 1
         total_pages = int(meta[3 * b:4 * b].sum())
         dmeta = self._pack.upload(meta)
         bt = self.alloc_manager.block_table
         grid = max(1, min(256, (total_pages + 1023) // 1024))  # about one page per thread
         base = dmeta.data_ptr()
-        _lib.check(
-            _lib.lib().mi_pack(
-                base, base + 4 * b, base + 8 * b, base + 12 * b, b, bt.table.data_ptr(), bt.stride, base + 16 * b,
+        args = [base, base + 4 * b, base + 8 * b, base + 12 * b, b, bt.table.data_ptr(), bt.stride, base + 16 * b,
                 base + 20 * b, self.kv_cache_config.page_size, qo.data_ptr(), kv_indptr.data_ptr(),
-                kv_indices.data_ptr(), last.data_ptr(), loc.data_ptr() if loc is not None else None, grid,
-                _lib.stream_ptr(self.device),
-            ),
-            "mi_pack",
+                kv_indices.data_ptr(), last.data_ptr(), loc.data_ptr() if loc is not None else None, grid]
+        if plan_wrapper is None:
+            _lib.check(_lib.lib().mi_pack(*args, _lib.stream_ptr(self.device)), "mi_pack")
+            return
+        w = plan_wrapper
+        ws = w._workspace
+        _lib.check(
+            _lib.lib().mi_pack_plan(*args, w.num_qo_heads, w.num_kv_heads, w.head_dim, ws.data_ptr(),
+                                    ws.numel() * ws.element_size(), _lib.stream_ptr(self.device)),
+            "mi_pack_plan",
         )
 
     def _plan_attention_impl(self, seq_lens, dtype, is_causal, write_store, label) -> None:
@@ -253,12 +259,18 @@ class BatchedCacheManager:
             last = wrapper._paged_kv_last_page_len_buf
             if total_pages > kv_indices.shape[0]:
                 raise ValueError(f"{total_pages} pages > wrapper max_num_pages {kv_indices.shape[0]}")
-            loc = torch.empty(b, 2, dtype=torch.long, device=self.device) if is_decode else None
+            loc = None
+            if is_decode:
+                loc = wrapper.kv_cache_locations if graph_static and b == wrapper.batch_size else \
+                    torch.empty(b, 2, dtype=torch.long, device=self.device)
         else:
             qo, kv_indptr, kv_indices, last, loc = _step_tensors(b, total_pages, is_decode, self.device)
-        self._launch_pack(meta, qo, kv_indptr, kv_indices, last, loc)
+        fused = isinstance(wrapper, PagedDecodeWrapper) and is_decode and (not graph_static or b == wrapper.batch_size)
+        self._launch_pack(meta, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=wrapper if fused else None)
         self._last_pack = (qo, kv_indptr, kv_indices[:total_pages], last, loc)
-        if isinstance(wrapper, PagedDecodeWrapper):
+        if fused:
+            wrapper._adopt_plan(kv_indptr, kv_indices[:total_pages], last, loc, dtype)
+        elif isinstance(wrapper, PagedDecodeWrapper):
             wrapper.plan(kv_indptr, kv_indices[:total_pages], last, kv_cache_locations=loc, dtype=dtype)
         else:
             wrapper.plan_device(qo, kv_indptr, kv_indices[:total_pages], last, total_tokens=int(meta[2 * b:3 * b].sum()),

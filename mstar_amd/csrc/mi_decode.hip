@@ -39,10 +39,10 @@
 
 #include "mi_common.h"
 #include "mi_internal.h"
+#include "mi_plan.h"
 
 namespace mi {
 
-constexpr int kRows = 16;             // MFMA N: query rows per wave
 constexpr int kMinChunkTokens = 1024;  // never split a request finer than this (4 waves x 256)
 
 
@@ -89,108 +89,7 @@ SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t w
   return L;
 }
 
-// Header words written by the plan kernel.
-enum { kHdrMagic = 0, kHdrBatch, kHdrChunks, kHdrChunkPages, kHdrMaxChunks };
-constexpr int32_t kPlanMagic = 0x4d494450;
-
-struct PlanParams {
-  const int32_t* qo_indptr;
-  const int32_t* kv_indptr;
-  const int32_t* kv_indices;
-  const int32_t* last_page_len;
-  int32_t batch, target, min_chunk_pages, max_chunks, group;
-  int32_t* hdr;
-  int32_t* chunk_indptr;
-  int4* work;
-  int64_t* kv_locations;
-};
-
-// Work list order: longest first.  Every request's full items (item_pages
-// pages) come first, then the requests' shorter remainder items in
-// descending size (64 size buckets, counting sort in LDS): the last
-// workgroups to start are the shortest, so the machine drains evenly instead
-// of waiting on full-size items that started late.  An item is
-// (request, index within the request, end page, items of the request); its
-// partial lives at chunk_indptr[request] + index whatever its list position.
-constexpr int kSizeBuckets = 64;
-
-__global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) {
-  __shared__ int smem[16];
-  __shared__ int s_bucket[kSizeBuckets];
-  const int total_pages = p.kv_indptr[p.batch] - p.kv_indptr[0];
-  int cp = (total_pages + p.target - 1) / p.target;
-  if (cp < p.min_chunk_pages) cp = p.min_chunk_pages;
-  if (threadIdx.x < kSizeBuckets) s_bucket[threadIdx.x] = 0;
-  __syncthreads();
-  auto items_of = [&](int b, int& np, int& n, int& full, int& rem_bucket) {
-    np = p.kv_indptr[b + 1] - p.kv_indptr[b];
-    n = np > 0 ? (np + cp - 1) / cp : 0;
-    if (p.qo_indptr) {  // ragged batch: only short-query requests belong to this kernel
-      const int qo_len = p.qo_indptr[b + 1] - p.qo_indptr[b];
-      if (qo_len <= 0 || qo_len * p.group > kRows) n = 0;
-    }
-    full = n > 0 ? np / cp : 0;
-    const int rem = n > 0 ? np - full * cp : 0;
-    rem_bucket = rem > 0 ? (int)(((int64_t)rem * kSizeBuckets - 1) / cp) : -1;
-  };
-  // pass 1: item offsets per request, full items in place, remainder histogram
-  int carry = 0, carry_full = 0;
-  for (int base = 0; base < p.batch; base += 1024) {
-    const int b = base + (int)threadIdx.x;
-    int np = 0, n = 0, full = 0, rb = -1;
-    if (b < p.batch) items_of(b, np, n, full, rb);
-    int total, total_full;
-    const int first = block_exclusive_scan_1024(n, total, smem) + carry;
-    const int ffirst = block_exclusive_scan_1024(full, total_full, smem) + carry_full;
-    if (b < p.batch) {
-      p.chunk_indptr[b] = first;
-      for (int c = 0; c < full && ffirst + c < p.max_chunks; ++c) p.work[ffirst + c] = make_int4(b, c, (c + 1) * cp, n);
-      if (rb >= 0) atomicAdd(&s_bucket[rb], 1);
-      if (p.kv_locations) {
-        int64_t page = -1, pos = -1;
-        if (np > 0) {
-          page = p.kv_indices[p.kv_indptr[b + 1] - 1];
-          pos = p.last_page_len[b] - 1;
-        }
-        p.kv_locations[2 * b] = page;
-        p.kv_locations[2 * b + 1] = pos;
-      }
-    }
-    carry += total;
-    carry_full += total_full;
-  }
-  __syncthreads();
-  // bucket start positions, largest bucket first, after all full items
-  if (threadIdx.x == 0) {
-    int off = carry_full;
-    for (int k = kSizeBuckets - 1; k >= 0; --k) {
-      const int c = s_bucket[k];
-      s_bucket[k] = off;
-      off += c;
-    }
-  }
-  __syncthreads();
-  // pass 2: remainder items
-  for (int base = 0; base < p.batch; base += 1024) {
-    const int b = base + (int)threadIdx.x;
-    if (b < p.batch) {
-      int np, n, full, rb;
-      items_of(b, np, n, full, rb);
-      if (rb >= 0) {
-        const int pos = atomicAdd(&s_bucket[rb], 1);
-        if (pos < p.max_chunks) p.work[pos] = make_int4(b, full, np, n);
-      }
-    }
-  }
-  if (threadIdx.x == 0) {
-    p.chunk_indptr[p.batch] = carry;
-    p.hdr[kHdrMagic] = kPlanMagic;
-    p.hdr[kHdrBatch] = p.batch;
-    p.hdr[kHdrChunks] = min(carry, p.max_chunks);
-    p.hdr[kHdrChunkPages] = cp;
-    p.hdr[kHdrMaxChunks] = p.max_chunks;
-  }
-}
+__global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) { decode_plan_body(p); }
 
 // ---------------------------------------------------------------- decode
 struct DecodeParams {
@@ -662,11 +561,11 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
 // ------------------------------------------------------------ host side
 static bool supported_head_dim(int d) { return d == 64 || d == 128 || d == 256; }
 
-int decode_plan_impl(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
-                     const int32_t* last_page_len, int32_t batch, int32_t page_size,
-                     int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
-                     int64_t* kv_locations, void* workspace, int64_t workspace_bytes,
-                     int64_t ws_offset, hipStream_t stream) {
+int decode_plan_params(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                       const int32_t* last_page_len, int32_t batch, int32_t page_size,
+                       int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                       int64_t* kv_locations, void* workspace, int64_t workspace_bytes,
+                       int64_t ws_offset, PlanParams* out) {
   if (batch < 0 || !kv_indptr || !last_page_len || !workspace) return MI_ERR_INVALID;
   if (batch > 0 && !kv_indices) return MI_ERR_INVALID;
   if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads) return MI_ERR_INVALID;
@@ -677,9 +576,10 @@ int decode_plan_impl(const int32_t* qo_indptr, const int32_t* kv_indptr, const i
   const SplitLayout L = split_layout(batch, num_kv_heads, head_dim, workspace_bytes - ws_offset);
   if (L.max_chunks <= batch || workspace_bytes < ws_offset + L.total) return MI_ERR_WORKSPACE;
   uint8_t* ws = (uint8_t*)workspace + ws_offset;
-  PlanParams pp;
+  PlanParams& pp = *out;
   pp.qo_indptr = qo_indptr;
   pp.kv_indptr = kv_indptr;
+  pp.num_pages = nullptr;
   pp.kv_indices = kv_indices;
   pp.last_page_len = last_page_len;
   pp.batch = batch;
@@ -691,6 +591,18 @@ int decode_plan_impl(const int32_t* qo_indptr, const int32_t* kv_indptr, const i
   pp.chunk_indptr = (int32_t*)(ws + L.chunk_indptr);
   pp.work = (int4*)(ws + L.work);
   pp.kv_locations = kv_locations;
+  return MI_OK;
+}
+
+int decode_plan_impl(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                     const int32_t* last_page_len, int32_t batch, int32_t page_size,
+                     int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int64_t* kv_locations, void* workspace, int64_t workspace_bytes,
+                     int64_t ws_offset, hipStream_t stream) {
+  PlanParams pp;
+  const int st = decode_plan_params(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
+                                    num_kv_heads, head_dim, kv_locations, workspace, workspace_bytes, ws_offset, &pp);
+  if (st != MI_OK) return st;
   hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(1024), 0, stream, pp);
   MI_CHECK_LAUNCH();
   return MI_OK;

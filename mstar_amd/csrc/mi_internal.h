@@ -20,6 +20,14 @@ int decode_plan_impl(const int32_t* qo_indptr, const int32_t* kv_indptr, const i
                      int64_t* kv_locations, void* workspace, int64_t workspace_bytes,
                      int64_t ws_offset, hipStream_t stream);
 
+// Checks the arguments and fills the plan kernel's parameters (no launch).
+struct PlanParams;
+int decode_plan_params(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                       const int32_t* last_page_len, int32_t batch, int32_t page_size,
+                       int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                       int64_t* kv_locations, void* workspace, int64_t workspace_bytes,
+                       int64_t ws_offset, PlanParams* out);
+
 enum : int { kPhaseAttend = 1, kPhaseMerge = 2 };
 
 int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,

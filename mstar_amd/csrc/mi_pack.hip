@@ -15,6 +15,7 @@
 // in LDS per page id; the grid is sized for about one page per thread).
 #include "mi_common.h"
 #include "mi_internal.h"
+#include "mi_plan.h"
 
 namespace mi {
 
@@ -37,7 +38,8 @@ struct PackParams {
   int32_t batch, page_size;
 };
 
-__global__ __launch_bounds__(kPackThreads) void pack_kernel(PackParams p) {
+// Workgroup `block` of `nblocks` packing workgroups.
+__device__ inline void pack_body(const PackParams& p, int block, int nblocks) {
   __shared__ int s_scan[16];
   __shared__ int s_off[kPackThreads + 1];  // window-relative exclusive page offsets
   __shared__ int s_slot[kPackThreads];
@@ -60,7 +62,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackParams p) {
     s_old[tid] = old;
     s_noff[tid] = ex_new;
     if (tid == 0) s_off[kPackThreads] = tot_kv;
-    if (blockIdx.x == 0 && live) {
+    if (block == 0 && live) {
       p.qo_indptr[b] = carry_qo + ex_qo;
       p.kv_indptr[b] = carry_kv + ex_kv;
       const int T = p.seq_len[b] + sl;
@@ -83,7 +85,7 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackParams p) {
     // flatten this window's page lists: kv_indices[carry_kv + f] for f < tot_kv;
     // pages past a request's table prefix come from new_pages and go into the table
     const int nreq = min(kPackThreads, p.batch - base);
-    for (int f = blockIdx.x * kPackThreads + tid; f < tot_kv; f += gridDim.x * kPackThreads) {
+    for (int f = block * kPackThreads + tid; f < tot_kv; f += nblocks * kPackThreads) {
       int lo = 0, hi = nreq - 1;  // last r with s_off[r] <= f
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -105,10 +107,23 @@ __global__ __launch_bounds__(kPackThreads) void pack_kernel(PackParams p) {
     carry_new += tot_new;
     __syncthreads();
   }
-  if (blockIdx.x == 0 && tid == 0) {
+  if (block == 0 && tid == 0) {
     p.qo_indptr[p.batch] = carry_qo;
     p.kv_indptr[p.batch] = carry_kv;
   }
+}
+
+__global__ __launch_bounds__(kPackThreads) void pack_kernel(PackParams p) { pack_body(p, blockIdx.x, gridDim.x); }
+
+// Pack and split-KV decode plan in one launch: workgroup 0 plans from the
+// per-request page counts (it needs none of the pack's outputs), the others
+// pack.
+__global__ __launch_bounds__(kPackThreads) void pack_plan_kernel(PackParams p, PlanParams pl) {
+  if (blockIdx.x == 0) {
+    decode_plan_body(pl);
+    return;
+  }
+  pack_body(p, blockIdx.x - 1, gridDim.x - 1);
 }
 
 __global__ __launch_bounds__(256) void block_table_update_kernel(int32_t* table, int64_t stride,
@@ -118,20 +133,17 @@ __global__ __launch_bounds__(256) void block_table_update_kernel(int32_t* table,
   if (i < n) table[(int64_t)slot[i] * stride + pos[i]] = page[i];
 }
 
-}  // namespace mi
-
-extern "C" int mi_pack(const int32_t* req_slot, const int32_t* seq_len, const int32_t* new_len,
-                       const int32_t* num_pages, int32_t batch, int32_t* block_table,
-                       int64_t block_table_stride, const int32_t* table_pages, const int32_t* new_pages,
-                       int32_t page_size, int32_t* qo_indptr, int32_t* kv_indptr, int32_t* kv_indices,
-                       int32_t* last_page_len, int64_t* kv_locations, int32_t grid_blocks, void* stream) {
-  using namespace mi;
+static int pack_params(const int32_t* req_slot, const int32_t* seq_len, const int32_t* new_len,
+                       const int32_t* num_pages, int32_t batch, int32_t* block_table, int64_t block_table_stride,
+                       const int32_t* table_pages, const int32_t* new_pages, int32_t page_size, int32_t* qo_indptr,
+                       int32_t* kv_indptr, int32_t* kv_indices, int32_t* last_page_len, int64_t* kv_locations,
+                       int32_t grid_blocks, PackParams* out) {
   if (batch < 0 || page_size <= 0 || grid_blocks <= 0 || block_table_stride <= 0) return MI_ERR_INVALID;
   if (!qo_indptr || !kv_indptr || !last_page_len) return MI_ERR_INVALID;
   if (batch > 0 && (!req_slot || !seq_len || !new_len || !num_pages || !block_table || !kv_indices))
     return MI_ERR_INVALID;
   if (table_pages && !new_pages) return MI_ERR_INVALID;
-  PackParams pp;
+  PackParams& pp = *out;
   pp.req_slot = req_slot;
   pp.seq_len = seq_len;
   pp.new_len = new_len;
@@ -147,7 +159,46 @@ extern "C" int mi_pack(const int32_t* req_slot, const int32_t* seq_len, const in
   pp.kv_locations = kv_locations;
   pp.batch = batch;
   pp.page_size = page_size;
+  return MI_OK;
+}
+
+}  // namespace mi
+
+extern "C" int mi_pack(const int32_t* req_slot, const int32_t* seq_len, const int32_t* new_len,
+                       const int32_t* num_pages, int32_t batch, int32_t* block_table,
+                       int64_t block_table_stride, const int32_t* table_pages, const int32_t* new_pages,
+                       int32_t page_size, int32_t* qo_indptr, int32_t* kv_indptr, int32_t* kv_indices,
+                       int32_t* last_page_len, int64_t* kv_locations, int32_t grid_blocks, void* stream) {
+  using namespace mi;
+  PackParams pp;
+  const int st = pack_params(req_slot, seq_len, new_len, num_pages, batch, block_table, block_table_stride,
+                             table_pages, new_pages, page_size, qo_indptr, kv_indptr, kv_indices, last_page_len,
+                             kv_locations, grid_blocks, &pp);
+  if (st != MI_OK) return st;
   hipLaunchKernelGGL(pack_kernel, dim3(grid_blocks), dim3(kPackThreads), 0, (hipStream_t)stream, pp);
+  MI_CHECK_LAUNCH();
+  return MI_OK;
+}
+
+extern "C" int mi_pack_plan(const int32_t* req_slot, const int32_t* seq_len, const int32_t* new_len,
+                            const int32_t* num_pages, int32_t batch, int32_t* block_table,
+                            int64_t block_table_stride, const int32_t* table_pages, const int32_t* new_pages,
+                            int32_t page_size, int32_t* qo_indptr, int32_t* kv_indptr, int32_t* kv_indices,
+                            int32_t* last_page_len, int64_t* kv_locations, int32_t grid_blocks,
+                            int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  using namespace mi;
+  PackParams pp;
+  int st = pack_params(req_slot, seq_len, new_len, num_pages, batch, block_table, block_table_stride, table_pages,
+                       new_pages, page_size, qo_indptr, kv_indptr, kv_indices, last_page_len, kv_locations,
+                       grid_blocks, &pp);
+  if (st != MI_OK) return st;
+  PlanParams pl;
+  st = decode_plan_params(nullptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
+                          num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, 0, &pl);
+  if (st != MI_OK) return st;
+  pl.num_pages = num_pages;  // the plan reads the step's page counts, not the pack's outputs
+  hipLaunchKernelGGL(pack_plan_kernel, dim3(grid_blocks + 1), dim3(kPackThreads), 0, (hipStream_t)stream, pp, pl);
   MI_CHECK_LAUNCH();
   return MI_OK;
 }

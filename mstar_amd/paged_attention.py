@@ -280,6 +280,27 @@ class PagedDecodeWrapper(_FusedRopeAppend):
         self._n_req = n_req
         self.dtype = dtype
 
+    def _adopt_plan(self, kv_indptr: torch.Tensor, kv_indices: torch.Tensor, last: torch.Tensor,
+                    kv_cache_locations: torch.Tensor, dtype: torch.dtype) -> None:
+        """Take a plan the caller already wrote into this wrapper's workspace
+        (``mi_pack_plan``: the packed device arrays and the split-KV plan of
+        one decode step), as if :meth:`plan` had been called with them."""
+        n_req = kv_indptr.shape[0] - 1
+        if self.use_cuda_graph:
+            if n_req != self.batch_size:
+                raise ValueError(f"CUDA-graph mode plans a fixed batch of {self.batch_size}, got {n_req}")
+            statics = (self._paged_kv_indptr_buf, self._paged_kv_indices_buf, self._paged_kv_last_page_len_buf)
+            if any(d.data_ptr() != t.data_ptr() for d, t in zip(statics, (kv_indptr, kv_indices, last))):
+                raise ValueError("a graph-mode plan must be packed into the wrapper's static buffers")
+            if kv_cache_locations.data_ptr() != self.kv_cache_locations.data_ptr():
+                self.kv_cache_locations[:n_req].copy_(kv_cache_locations)
+            kv_indptr, kv_indices, last = statics
+        else:
+            self.kv_cache_locations = kv_cache_locations
+        self._indptr, self._indices, self._last = kv_indptr, kv_indices, last
+        self._n_req = n_req
+        self.dtype = dtype
+
     # --------------------------------------------------------------- run
     def run(self, q: torch.Tensor, kv_cache_layer: torch.Tensor, k_scale: torch.Tensor | None = None,
             v_scale: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:

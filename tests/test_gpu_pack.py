@@ -138,3 +138,52 @@ def test_decode_plan_partition(gpu):
         else:
             exp.append([int(kv_indices[kv_indptr[r + 1] - 1]), int(last[r]) - 1])
     assert loc.cpu().tolist() == exp
+
+
+def test_pack_plan_matches_pack_then_plan(gpu):
+    """mi_pack_plan (one launch) == mi_pack followed by mi_decode_plan on the packed arrays."""
+    from mstar_amd.cache_manager import _step_tensors
+
+    ps, hq, hkv, d = 16, 32, 4, 128
+    rng = np.random.default_rng(7)
+    lens = [0, 1, 17, 300, 5000, 32768, 4096, 77] + rng.integers(1, 20000, size=300).tolist()
+    b = len(lens)
+    npages = [(t + ps - 1) // ps for t in lens]
+    pool = torch.randperm(sum(npages) + 64, generator=torch.Generator().manual_seed(3)).numpy().astype(np.int32)
+    stride = max(npages) + 1
+    table = torch.zeros(b, stride, dtype=torch.int32, device=gpu)
+    meta = np.empty((5, b), dtype=np.int32)
+    meta[0] = np.arange(b)                      # slots
+    meta[1] = np.maximum(np.array(lens) - 1, 0)  # seq_len before the step
+    meta[2] = 1                                  # one new token each
+    meta[3] = npages
+    meta[4] = 0                                  # nothing in the table yet: every page is new
+    flat = np.concatenate([meta.reshape(-1), pool[:sum(npages)]])
+    dmeta = torch.from_numpy(flat).to(gpu)
+    base = dmeta.data_ptr()
+    outs = []
+    for fused in (False, True):
+        ws = workspace(gpu, 64 << 20)
+        ws.zero_()
+        table.zero_()
+        qo, ip, idx, last, loc = _step_tensors(b, sum(npages), True, gpu)
+        args = [base, base + 4 * b, base + 8 * b, base + 12 * b, b, table.data_ptr(), stride, base + 16 * b,
+                base + 20 * b, ps, qo.data_ptr(), ip.data_ptr(), idx.data_ptr(), last.data_ptr(), loc.data_ptr(), 7]
+        L = _lib.lib()
+        if fused:
+            _lib.check(L.mi_pack_plan(*args, hq, hkv, d, ws.data_ptr(), ws.numel(), _lib.stream_ptr()), "pack_plan")
+        else:
+            _lib.check(L.mi_pack(*args, _lib.stream_ptr()), "pack")
+            _lib.check(L.mi_decode_plan(None, ip.data_ptr(), idx.data_ptr(), last.data_ptr(), b, ps, hq, hkv, d, None,
+                                        ws.data_ptr(), ws.numel(), _lib.stream_ptr()), "plan")
+        torch.cuda.synchronize()
+        hdr, ci, wk, _ = _split_layout(b, hkv, d)
+        h = ws[hdr:hdr + 20].cpu().view(torch.int32).tolist()
+        cptr = ws[ci:ci + 4 * (b + 1)].cpu().view(torch.int32).tolist()
+        work = ws[wk:wk + 16 * h[2]].cpu().view(torch.int32).numpy().reshape(-1, 4)
+        outs.append((h, cptr, sorted(map(tuple, work.tolist())), work[:, :2].tolist(),
+                     [t.cpu().tolist() for t in (qo, ip, idx, last, loc)], table.cpu().tolist()))
+    (h0, c0, w0, o0, p0, t0), (h1, c1, w1, o1, p1, t1) = outs
+    assert h0 == h1 and c0 == c1 and w0 == w1 and p0 == p1 and t0 == t1
+    nfull = sum(1 for r, k, e, n in w0 if e == (k + 1) * h0[3])
+    assert o0[:nfull] and sorted(map(tuple, o0[:nfull])) == sorted(map(tuple, o1[:nfull]))  # full items first in both
