@@ -2,11 +2,11 @@
 //
 // Replaces FlashInferPrefillWrapper.plan/run (mstar/utils/flashinfer_utils.py:162-269).
 //
-// plan:  token_map_kernel writes the per-new-token (page, slot) map of
-//        flashinfer_utils.py:211-256; prefill_plan_kernel lists the tiles of
-//        every long-query request, costs them, and cuts the (kv-head, tile)
-//        units into 8 cost-balanced per-XCD queues; short-query requests
-//        (qo_len * group <= 16, e.g. the decode rows of a mixed batch) get a
+// plan:  one launch (prefill_plan_kernel): the token map (the per-new-token
+//        (page, slot) of flashinfer_utils.py:211-256), the tiles of every
+//        long-query request, costed and cut as (kv-head, tile) units into 8
+//        cost-balanced per-XCD queues, and, for the short-query requests
+//        (qo_len * group <= 16, e.g. the decode rows of a mixed batch), a
 //        split-KV plan for the decode kernel in the same workspace.
 // run:   mi_prefill_short (decode kernel + merge for the short-query
 //        requests) and mi_prefill_tiles (prefill_kernel).
@@ -29,6 +29,7 @@
 // per-head scales multiply the scores and the output.
 #include "mi_common.h"
 #include "mi_internal.h"
+#include "mi_plan.h"
 
 namespace mi {
 
@@ -68,12 +69,26 @@ static PrefillLayout prefill_layout(int32_t batch, int32_t max_qo_tokens, int32_
 }
 
 // ------------------------------------------------------------ token map
-__global__ __launch_bounds__(256) void token_map_kernel(const int32_t* qo_indptr, const int32_t* kv_indptr,
-                                                        const int32_t* kv_indices, const int32_t* last_page_len,
-                                                        int32_t batch, int32_t page_size, int64_t* t2p,
-                                                        int64_t* t2c, int32_t map_len) {
-  const int t = blockIdx.x * 256 + threadIdx.x;
-  if (t >= map_len) return;
+struct TokenMapArgs {
+  const int32_t* qo_indptr;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* last_page_len;
+  int32_t batch, page_size;
+  int64_t* t2p;
+  int64_t* t2c;
+  int32_t map_len;
+};
+
+__device__ inline void token_map_body(const TokenMapArgs& m, int t) {
+  const int32_t* qo_indptr = m.qo_indptr;
+  const int32_t* kv_indptr = m.kv_indptr;
+  const int32_t* kv_indices = m.kv_indices;
+  const int32_t* last_page_len = m.last_page_len;
+  const int batch = m.batch, page_size = m.page_size;
+  int64_t* t2p = m.t2p;
+  int64_t* t2c = m.t2c;
+  if (t >= m.map_len) return;
   const int total = qo_indptr[batch];
   if (t >= total) {  // graph-mode tail (flashinfer_utils.py:251-253)
     t2p[t] = 0;
@@ -114,74 +129,111 @@ __device__ int pf_tile_cost(int kv_len, int qo_len, int rows_total, int row0, in
   return kv_end > 0 ? (kv_end + kPfKeys - 1) / kPfKeys : 0;
 }
 
-__global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* qo_indptr, const int32_t* kv_indptr,
-                                                            const int32_t* last_page_len, int32_t batch,
-                                                            int32_t page_size, int32_t group, int32_t nkv,
-                                                            int32_t tile_rows, int32_t max_tiles, int32_t causal,
-                                                            int32_t* hdr, int2* tiles, int32_t* tcum,
-                                                            int32_t* order, int32_t* ctr) {
+struct PfPlanArgs {
+  const int32_t* qo_indptr;
+  const int32_t* kv_indptr;
+  const int32_t* last_page_len;
+  int32_t batch, page_size, group, nkv, tile_rows, max_tiles, causal;
+  int32_t* hdr;
+  int2* tiles;
+  int32_t* tcum;
+  int32_t* order;
+  int32_t* ctr;
+};
+
+// One 1024-thread workgroup.  Requests go in windows of 1024 (one per
+// thread: tile count, exclusive scan); the window's tiles are then listed
+// 1024 at a time, one per thread, each finding its request by a binary
+// search over the window's scan in LDS, so no thread loops over a long
+// request's tiles.
+__device__ inline void prefill_plan_body(const PfPlanArgs& a) {
   __shared__ int smem[16];
   __shared__ int s_cut[9];
+  __shared__ int s_first[1025];  // window-relative first tile of each request, [1024] = window total
+  __shared__ int s_kvl[1024], s_qol[1024];
   __shared__ int s_bin[8 * 1024];
+  const int tid = (int)threadIdx.x;
+  const int group = a.group, tile_rows = a.tile_rows, causal = a.causal, max_tiles = a.max_tiles;
   int carry = 0, carry_cost = 0;
-  for (int base = 0; base < batch; base += 1024) {
-    const int b = base + (int)threadIdx.x;
-    int n = 0, cost = 0, kv_len = 0, qo_len = 0;
-    if (b < batch) {
-      qo_len = qo_indptr[b + 1] - qo_indptr[b];
+  for (int base = 0; base < a.batch; base += 1024) {
+    const int b = base + tid;
+    int n = 0;
+    if (b < a.batch) {
+      const int qo_len = a.qo_indptr[b + 1] - a.qo_indptr[b];
       const int rows = qo_len * group;
       n = rows > kShortRows ? (rows + tile_rows - 1) / tile_rows : 0;
-      kv_len = (kv_indptr[b + 1] - kv_indptr[b] - 1) * page_size + last_page_len[b];
-      for (int i = 0; i < n; ++i)
-        cost += pf_tile_cost(kv_len, qo_len, rows, (n - 1 - i) * tile_rows, tile_rows, group, causal);
+      s_qol[tid] = qo_len;
+      s_kvl[tid] = (a.kv_indptr[b + 1] - a.kv_indptr[b] - 1) * a.page_size + a.last_page_len[b];
     }
-    int total, total_cost;
-    const int first = block_exclusive_scan_1024(n, total, smem) + carry;
-    int cum = block_exclusive_scan_1024(cost, total_cost, smem) + carry_cost;
-    for (int i = 0; i < n && first + i < max_tiles; ++i) {
-      const int row0 = (n - 1 - i) * tile_rows;
-      tiles[first + i] = make_int2(b, row0);
-      tcum[first + i] = cum;
-      cum += pf_tile_cost(kv_len, qo_len, qo_len * group, row0, tile_rows, group, causal);
+    int total;
+    s_first[tid] = block_exclusive_scan_1024(n, total, smem);
+    if (tid == 0) s_first[1024] = total;
+    __syncthreads();
+    const int nreq = min(1024, a.batch - base);
+    for (int j0 = 0; j0 < total; j0 += 1024) {
+      const int j = j0 + tid;
+      int cost = 0, r = 0, row0 = 0;
+      if (j < total) {
+        int lo = 0, hi = nreq - 1;  // last request whose first tile is <= j (it has tiles)
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (s_first[mid] <= j) lo = mid; else hi = mid - 1;
+        }
+        r = lo;
+        const int nr = s_first[r + 1] - s_first[r];
+        row0 = (nr - 1 - (j - s_first[r])) * tile_rows;
+        cost = pf_tile_cost(s_kvl[r], s_qol[r], s_qol[r] * group, row0, tile_rows, group, causal);
+      }
+      int tot_cost;
+      const int cum = block_exclusive_scan_1024(cost, tot_cost, smem);
+      if (j < total && carry + j < max_tiles) {
+        a.tiles[carry + j] = make_int2(base + r, row0);
+        a.tcum[carry + j] = carry_cost + cum;
+      }
+      carry_cost += tot_cost;
     }
     carry += total;
-    carry_cost += total_cost;
+    __syncthreads();  // s_first / s_kvl / s_qol are rewritten by the next window
   }
   const int n_tiles = min(carry, max_tiles);
-  if (threadIdx.x == 0) tcum[n_tiles] = carry_cost;  // truncated lists keep a consistent prefix end
+  if (tid == 0) a.tcum[n_tiles] = carry_cost;  // truncated lists keep a consistent prefix end
+  __threadfence_block();
   __syncthreads();
-  const int64_t ct = tcum[n_tiles];
-  const int64_t units = (int64_t)n_tiles * nkv;
-  const int64_t total = ct * nkv;
-  if (threadIdx.x == 0) {
-    hdr[0] = n_tiles;
-    hdr[1] = (int32_t)units;
+  const int64_t ct = carry_cost;
+  const int64_t units = (int64_t)n_tiles * a.nkv;
+  const int64_t total = ct * a.nkv;
+  if (tid == 0) {
+    a.hdr[0] = n_tiles;
+    a.hdr[1] = (int32_t)units;
   }
-  if (threadIdx.x <= 8) {
-    const int x = threadIdx.x;
-    int64_t u0 = units;
-    if (x == 0) {
-      u0 = 0;
-    } else if (x < 8 && total > 0) {
-      // first unit whose cost prefix reaches ceil(x * total / 8)
-      const int64_t target = (x * total + 7) / 8;
-      int64_t lo = 0, hi = units;
-      while (lo < hi) {
-        const int64_t mid = (lo + hi) >> 1;
-        const int64_t h = mid / n_tiles, t = mid - h * n_tiles;
-        if (h * ct + tcum[t] >= target) hi = mid; else lo = mid + 1;
+  // Queue cuts: queue x starts at the first unit whose cost prefix
+  // h*ct + tcum[t] (unit u = h*n_tiles + t) reaches ceil(x * total / 8).
+  // The prefix never decreases, so that unit is the one u with
+  // prefix(u-1) < target <= prefix(u); every thread tests its units.
+  if (tid <= 8) s_cut[tid] = tid == 0 ? 0 : (int)units;
+  __syncthreads();
+  if (total > 0) {
+    auto prefix = [&](int64_t u) -> int64_t {
+      const int64_t h = u / n_tiles, t = u - h * n_tiles;
+      return h * ct + a.tcum[t];
+    };
+    for (int64_t u = 1 + tid; u < units; u += 1024) {
+      const int64_t pu = prefix(u), pp = prefix(u - 1);
+#pragma unroll
+      for (int x = 1; x < 8; ++x) {
+        const int64_t target = (x * total + 7) / 8;
+        if (pp < target && target <= pu) s_cut[x] = (int)u;
       }
-      u0 = lo;
     }
-    hdr[8 + x] = (int32_t)u0;
-    s_cut[x] = (int)u0;
   }
   __syncthreads();
+  if (tid <= 8) a.hdr[8 + tid] = s_cut[tid];
   // Within each queue, units go heaviest first: one counting sort over
   // (queue, 1023 - min(cost, 1023)) keys in LDS.  Queues are contiguous unit
   // ranges, so the sorted positions of queue x start at its first unit.
-  for (int i = threadIdx.x; i < 8 * 1024; i += 1024) s_bin[i] = 0;
+  for (int i = tid; i < 8 * 1024; i += 1024) s_bin[i] = 0;
   __syncthreads();
+  const int32_t* tcum = a.tcum;
   auto key_of = [&](int u) {
     int x = 0;
 #pragma unroll
@@ -189,26 +241,38 @@ __global__ __launch_bounds__(1024) void prefill_plan_kernel(const int32_t* qo_in
     const int t = u % n_tiles;
     return x * 1024 + 1023 - min(tcum[t + 1] - tcum[t], 1023);
   };
-  for (int u = (int)threadIdx.x; u < (int)units; u += 1024) atomicAdd(&s_bin[key_of(u)], 1);
+  for (int u = tid; u < (int)units; u += 1024) atomicAdd(&s_bin[key_of(u)], 1);
   __syncthreads();
   {
     int loc[8], sum = 0;  // thread t owns bins [8t, 8t + 8)
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       loc[k] = sum;
-      sum += s_bin[8 * threadIdx.x + k];
+      sum += s_bin[8 * tid + k];
     }
     int tot;
     const int base = block_exclusive_scan_1024(sum, tot, smem);
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 8; ++k) s_bin[8 * threadIdx.x + k] = base + loc[k];
+    for (int k = 0; k < 8; ++k) s_bin[8 * tid + k] = base + loc[k];
   }
   __syncthreads();
-  for (int u = (int)threadIdx.x; u < (int)units; u += 1024) order[atomicAdd(&s_bin[key_of(u)], 1)] = u;
-  if (threadIdx.x < 9) ctr[threadIdx.x * kCtrStride] = 0;  // queues of the first run
+  for (int u = tid; u < (int)units; u += 1024) a.order[atomicAdd(&s_bin[key_of(u)], 1)] = u;
+  if (tid < 9) a.ctr[tid * kCtrStride] = 0;  // queues of the first run
 }
 
+// The whole plan in one launch: workgroup 0 lists and orders the MFMA tiles,
+// workgroup 1 builds the split-KV plan of the short-query requests, the
+// others write the token map (1024 tokens each).  None reads another's output.
+__global__ __launch_bounds__(1024) void prefill_plan_kernel(PfPlanArgs a, PlanParams d, TokenMapArgs m) {
+  if (blockIdx.x == 0) {
+    prefill_plan_body(a);
+  } else if (blockIdx.x == 1) {
+    decode_plan_body(d);
+  } else {
+    token_map_body(m, ((int)blockIdx.x - 2) * 1024 + (int)threadIdx.x);
+  }
+}
 
 // ------------------------------------------------------------ attention
 struct PrefillParams {
@@ -672,20 +736,41 @@ extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
   if (G > kShortRows) return MI_ERR_UNSUPPORTED;
   const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, num_kv_heads, head_dim);
   if (workspace_bytes < L.split) return MI_ERR_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
   uint8_t* ws = (uint8_t*)workspace;
-  if (token_map_len > 0) {
-    hipLaunchKernelGGL(token_map_kernel, dim3((token_map_len + 255) / 256), dim3(256), 0, s, qo_indptr, kv_indptr,
-                       kv_indices, last_page_len, batch, page_size, token_to_page, token_to_cache, token_map_len);
-  }
-  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(1024), 0, s, qo_indptr, kv_indptr, last_page_len, batch,
-                     page_size, G, num_kv_heads, pf_rows(head_dim), L.max_tiles, /*cost model: causal*/ 1,
-                     (int32_t*)(ws + L.hdr),
-                     (int2*)(ws + L.tiles), (int32_t*)(ws + L.tcum), (int32_t*)(ws + L.order),
-                     (int32_t*)(ws + L.ctr));
+  PlanParams d;
+  const int st = decode_plan_params(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
+                                    num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, L.split, &d);
+  if (st != MI_OK) return st;
+  PfPlanArgs a;
+  a.qo_indptr = qo_indptr;
+  a.kv_indptr = kv_indptr;
+  a.last_page_len = last_page_len;
+  a.batch = batch;
+  a.page_size = page_size;
+  a.group = G;
+  a.nkv = num_kv_heads;
+  a.tile_rows = pf_rows(head_dim);
+  a.max_tiles = L.max_tiles;
+  a.causal = 1;  // cost model: causal
+  a.hdr = (int32_t*)(ws + L.hdr);
+  a.tiles = (int2*)(ws + L.tiles);
+  a.tcum = (int32_t*)(ws + L.tcum);
+  a.order = (int32_t*)(ws + L.order);
+  a.ctr = (int32_t*)(ws + L.ctr);
+  TokenMapArgs m;
+  m.qo_indptr = qo_indptr;
+  m.kv_indptr = kv_indptr;
+  m.kv_indices = kv_indices;
+  m.last_page_len = last_page_len;
+  m.batch = batch;
+  m.page_size = page_size;
+  m.t2p = token_to_page;
+  m.t2c = token_to_cache;
+  m.map_len = token_map_len;
+  const int grid = 2 + (token_map_len + 1023) / 1024;
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(grid), dim3(1024), 0, (hipStream_t)stream, a, d, m);
   MI_CHECK_LAUNCH();
-  return decode_plan_impl(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
-                          num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, L.split, s);
+  return MI_OK;
 }
 
 namespace mi {

@@ -198,3 +198,67 @@ def test_prefill_graph_mode_tail_and_padding(gpu):
     torch.cuda.synchronize()
     written = int((cache[:, 0].float().abs().sum(dim=(2, 3)) != 0).sum().item())
     assert written == 30
+
+
+def test_prefill_plan_tiles_costs_and_queues(gpu):
+    """The plan's tile list, cost prefix, per-XCD queue cuts and unit order, read from the
+    workspace and checked against a host listing (more than 1024 requests and more than
+    1024 tiles in one request, so both of the plan's loops take several rounds)."""
+    hq, hkv, d, ps = 28, 4, 128, 16
+    g_ = hq // hkv
+    rng = np.random.default_rng(11)
+    b = 1500
+    new = np.ones(b, dtype=np.int64)
+    kvl = rng.integers(1, 3000, size=b)
+    for r, (qn, kn) in {3: (40000, 41000), 700: (513, 600), 1100: (3, 3), 1499: (2048, 9000)}.items():
+        new[r], kvl[r] = qn, kn
+    qo, kv_indptr, kv_indices, last = custom_batch(kvl, ps, int(sum(-(-kvl // ps))) + 4, 5, new_lens=new)
+    w = FlashInferPrefillWrapper(workspace(gpu, 512 << 20), hq, hkv, d, ps, device=gpu)
+    w.plan(torch.as_tensor(qo), torch.as_tensor(kv_indptr), torch.as_tensor(kv_indices), torch.as_tensor(last),
+           causal=True)
+    torch.cuda.synchronize()
+    # host listing: tiles of 256 rows, request order, last rows first; cost = 32-key steps to the causal limit
+    exp_tiles, exp_cost = [], []
+    for r in range(b):
+        rows = int(new[r]) * g_
+        if rows <= 16:
+            continue
+        n = -(-rows // 256)
+        for i in range(n):
+            row0 = (n - 1 - i) * 256
+            last_row = min(row0 + 256, rows) - 1
+            kv_end = min(int(kvl[r]), int(kvl[r]) - int(new[r]) + last_row // g_ + 1)
+            exp_tiles.append((r, row0))
+            exp_cost.append(-(-kv_end // 32) if kv_end > 0 else 0)
+    nt = len(exp_tiles)
+    assert max(-(-int(new[r]) * g_ // 256) for r in range(b)) > 1024
+    max_tok = w._plan_max_tokens
+    mt = -(-max_tok * g_ // 256) + b
+    al = lambda x: -(-x // 256) * 256
+    o_tiles = 256 + 9 * 32 * 4
+    o_tcum = al(o_tiles + 8 * mt)
+    o_order = al(o_tcum + 4 * (mt + 1))
+    ws = w._workspace
+    i32 = lambda off, n: ws[off:off + 4 * n].cpu().view(torch.int32).numpy().astype(np.int64)
+    hdr = i32(0, 17)
+    units = nt * hkv
+    assert hdr[0] == nt and hdr[1] == units
+    tiles = i32(o_tiles, 2 * nt).reshape(-1, 2)
+    assert [tuple(t) for t in tiles.tolist()] == exp_tiles
+    tcum = i32(o_tcum, nt + 1)
+    assert tcum.tolist() == [0] + np.cumsum(exp_cost).tolist()
+    ct = int(tcum[nt])
+    total = ct * hkv
+    prefix = np.array([h * ct + tcum[t] for h in range(hkv) for t in range(nt)] + [total])
+    cuts = hdr[8:17].tolist()
+    assert cuts[0] == 0 and cuts[8] == units and cuts == sorted(cuts)
+    for x in range(1, 8):
+        target = -(-x * total // 8)
+        assert cuts[x] == int(np.argmax(prefix >= target))
+    order = i32(o_order, units)
+    cost_u = np.array([exp_cost[u % nt] for u in range(units)])
+    for x in range(8):
+        seg = order[cuts[x]:cuts[x + 1]]
+        assert sorted(seg.tolist()) == list(range(cuts[x], cuts[x + 1]))
+        keys = np.minimum(cost_u[seg], 1023)
+        assert (np.diff(keys) <= 0).all(), f"queue {x} not heaviest first"
