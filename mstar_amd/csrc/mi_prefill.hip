@@ -641,7 +641,12 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         const int ii = i + u;
         if (ii >= n) break;
         const int T = t0 + ii;
+        // Tile T+1 goes into the stage tile T-2 used, which no wave reads in
+        // this step; each group stores it (and issues the loads of tile T+4)
+        // in its vector half, under the other group's MFMA work.
         if (grp_a) {
+          store_tile(min(T + 1, tl), rr[(u + 2) % 3], (u + 2) % 3);
+          load_tile(min(T + 4, tl), rr[(u + 2) % 3]);
           sm_max(T - 1, sc);
           sm_exp(sc, pbk);
         }
@@ -650,11 +655,11 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         qk((u + 1) % 3, sc);       // stage of tile T = ii % 3
         if constexpr (VPRE) vfrag((u + 1) % 3, va);
         if (!grp_a) {
+          store_tile(min(T + 1, tl), rr[(u + 2) % 3], (u + 2) % 3);
+          load_tile(min(T + 4, tl), rr[(u + 2) % 3]);
           sm_max(T, sc);
           sm_exp(sc, pbk);
         }
-        store_tile(min(T + 1, tl), rr[(u + 2) % 3], (u + 2) % 3);
-        load_tile(min(T + 4, tl), rr[(u + 2) % 3]);
         __syncthreads();
       }
     }
