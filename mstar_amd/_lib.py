@@ -254,9 +254,36 @@ class PinnedUploader:
         return dev[:n]
 
 
+_desc_cache: dict = {}
+
+
+def _scale_key(s: torch.Tensor | None):
+    if s is None:
+        return None
+    return (s.data_ptr(), s.dtype, s.numel(), s.is_contiguous(), s.device)
+
+
 def paged_kv_desc(kv_cache_layer: torch.Tensor, k_scale: torch.Tensor | None = None,
                   v_scale: torch.Tensor | None = None) -> MiPagedKV:
-    """Describe one KV layer ``[max_pages, 2, page_size, num_kv_heads, head_dim]``."""
+    """Describe one KV layer ``[max_pages, 2, page_size, num_kv_heads, head_dim]``.
+
+    Descriptors are kept by everything they are built and checked from
+    (address, shape, strides, dtype, and the scales' address, dtype, size,
+    layout and device), so a layer seen before costs one dictionary lookup.
+    """
+    key = (kv_cache_layer.data_ptr(), kv_cache_layer.shape, kv_cache_layer.stride(), kv_cache_layer.dtype,
+           kv_cache_layer.device, _scale_key(k_scale), _scale_key(v_scale))
+    d = _desc_cache.get(key)
+    if d is None:
+        d = _build_paged_kv_desc(kv_cache_layer, k_scale, v_scale)
+        if len(_desc_cache) >= 256:
+            _desc_cache.clear()
+        _desc_cache[key] = d
+    return d
+
+
+def _build_paged_kv_desc(kv_cache_layer: torch.Tensor, k_scale: torch.Tensor | None,
+                         v_scale: torch.Tensor | None) -> MiPagedKV:
     if kv_cache_layer.dim() != 5 or kv_cache_layer.shape[1] != 2:
         raise ValueError(
             f"kv_cache_layer must be [max_pages, 2, page_size, num_kv_heads, head_dim], got {tuple(kv_cache_layer.shape)}"

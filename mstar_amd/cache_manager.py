@@ -170,7 +170,7 @@ class BatchedCacheManager:
             raise ValueError(f"{len(seq_lens)} seq_lens for {n} requests")
         if states is None:
             states = [self._get_state(rid, label) for rid, label in entries]
-        seq = np.fromiter((st.seq_len for st in states), dtype=np.int64, count=n)
+        seq = np.array([st.seq_len for st in states], dtype=np.int64)
         sl = np.asarray(seq_lens, dtype=np.int64).reshape(n)
         self.alloc_manager.alloc_batch(entries, states, seq + sl)
         slots, npg, old, new_pages = self.alloc_manager.block_table.prepare_meta(states)

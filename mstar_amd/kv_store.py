@@ -359,7 +359,7 @@ class PagedAllocationManager:
         """
         ps = self.config.page_size
         with self._lock:
-            npg = np.fromiter((len(st.page_indices) for st in states), dtype=np.int64, count=len(states))
+            npg = np.array([len(st.page_indices) for st in states], dtype=np.int64)
             need = (np.asarray(seq_lens_after, dtype=np.int64) + ps - 1) // ps - npg
             idx = np.flatnonzero(need > 0).tolist()
             if not idx:
