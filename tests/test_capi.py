@@ -91,6 +91,26 @@ def test_unsupported_shapes_are_reported(L):
 
 
 
+def test_pack_plan_arguments_are_checked(L):
+    """mi_pack_plan: the pack's checks, then the decode plan's (heads, head_dim, workspace)."""
+    buf = (ctypes.c_int32 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    MI_ERR_WORKSPACE = -3
+
+    def call(batch=4, grid=1, hq=32, hkv=4, d=128, ws=p, ws_bytes=1 << 30, ps=16):
+        return L.mi_pack_plan(p, p, p, p, batch, p, 8, None, None, ps, p, p, p, p, None, grid, hq, hkv, d, ws,
+                              ws_bytes, None)
+
+    assert call(batch=-1) == MI_ERR_INVALID           # pack: negative batch
+    assert call(grid=0) == MI_ERR_INVALID             # pack: no workgroups
+    assert call(ws=None) == MI_ERR_INVALID            # plan: no workspace
+    assert call(hq=30, hkv=4) == MI_ERR_INVALID       # plan: heads not a multiple
+    assert call(hq=64, hkv=2) == MI_ERR_UNSUPPORTED   # plan: GQA group 32 > 16
+    assert call(d=96) == MI_ERR_UNSUPPORTED           # plan: head_dim
+    assert call(ps=8) == MI_ERR_UNSUPPORTED           # plan: page size not a multiple of 16
+    assert call(ws_bytes=1024) == MI_ERR_WORKSPACE    # plan: workspace too small
+
+
 def test_rope_arguments_are_checked(L):
     buf = (ctypes.c_int32 * 64)()
     p = ctypes.cast(buf, ctypes.c_void_p)
