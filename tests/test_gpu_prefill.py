@@ -262,3 +262,33 @@ def test_prefill_plan_tiles_costs_and_queues(gpu):
         assert sorted(seg.tolist()) == list(range(cuts[x], cuts[x + 1]))
         keys = np.minimum(cost_u[seg], 1023)
         assert (np.diff(keys) <= 0).all(), f"queue {x} not heaviest first"
+
+
+@pytest.mark.parametrize("hq,hkv,d,causal", [(28, 4, 128, True), (28, 4, 128, False), (8, 1, 256, True)])
+def test_prefill_long_context_page_chunks(gpu, hq, hkv, d, causal):
+    """Contexts longer than the 2048 page ids the kernel stages in LDS at once (several
+    page chunks per tile), against fp32 attention on the GPU."""
+    ps = 16
+    kv_lens = [40000, 33000, 70000, 2100]
+    new_lens = [64, 300, 5, 2100]
+    qo, kv_indptr, kv_indices, last = custom_batch(kv_lens, ps, sum(-(-np.array(kv_lens) // ps)) + 8, 21,
+                                                   new_lens=new_lens)
+    pool = int(kv_indices.max()) + 1
+    log(f"long context hq={hq} hkv={hkv} d={d} causal={causal}: kv={kv_lens} new={new_lens}")
+    cache = torch.empty(pool, 2, ps, hkv, d, dtype=torch.bfloat16, device=gpu)
+    cache.normal_(generator=torch.Generator(device=gpu).manual_seed(5))
+    g = torch.Generator().manual_seed(6)
+    ntok = int(qo[-1])
+    q = torch.randn(ntok, hq, d, generator=g).to(torch.bfloat16).to(gpu)
+    k = torch.randn(ntok, hkv, d, generator=g).to(torch.bfloat16).to(gpu)
+    v = torch.randn(ntok, hkv, d, generator=g).to(torch.bfloat16).to(gpu)
+    w = FlashInferPrefillWrapper(workspace(gpu, 512 << 20), hq, hkv, d, ps, device=gpu)
+    w.plan(torch.as_tensor(qo), torch.as_tensor(kv_indptr), torch.as_tensor(kv_indices), torch.as_tensor(last),
+           causal=causal)
+    w.set_kv_cache(cache, k, v)
+    out = w.run(q, cache)
+    ref = _torch_ref_gpu(q, cache, qo, kv_indptr, kv_indices, last, causal, hq, hkv)
+    torch.cuda.synchronize()
+    err = (out.float() - ref).abs().max().item()
+    log(f"  max_abs={err:.3e}")
+    assert err < TOL
