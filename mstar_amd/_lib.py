@@ -222,7 +222,11 @@ class PinnedUploader:
 
     Buffers alternate, so writing this call's data waits only for the copy
     issued two calls ago; the copy is one hipMemcpyAsync on the current
-    stream into a fresh device tensor.
+    stream into a fresh device tensor.  The staging buffers are never handed
+    back to torch's pinned-memory cache while a copy from them may be
+    pending (the raw copy records nothing there): use the per-device
+    instance from :func:`uploader`, which lives for the process, and a buffer
+    is only replaced after its last copy has finished.
     """
 
     def __init__(self, device: torch.device):
@@ -230,28 +234,45 @@ class PinnedUploader:
         self._bufs: list = [None, None]
         self._events: list = [None, None]
         self._i = 0
+        self._lock = threading.Lock()
 
     def upload(self, arr) -> torch.Tensor:
         n = int(arr.size)
-        i = self._i
-        self._i ^= 1
-        buf = self._bufs[i]
-        if buf is None or buf[1].size < n:
-            t = torch.empty(max(n, 4096), dtype=torch.int32, pin_memory=True)
-            buf = self._bufs[i] = (t, t.numpy())
-            self._events[i] = None
-        ev = self._events[i]
-        if ev is not None:
-            ev.synchronize()  # the copy that last read this buffer is done
-        buf[1][:n] = arr
-        dev = torch.empty(max(n, 1), dtype=torch.int32, device=self.device)
-        stream = stream_ptr(self.device)
-        if n:
-            memcpy_h2d_async(dev.data_ptr(), buf[0].data_ptr(), 4 * n, stream)
-        if ev is None:
-            ev = self._events[i] = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.device))
+        with self._lock:
+            i = self._i
+            self._i ^= 1
+            ev = self._events[i]
+            if ev is not None:
+                ev.synchronize()  # the copy that last read this buffer is done
+            buf = self._bufs[i]
+            if buf is None or buf[1].size < n:
+                t = torch.empty(max(n, 4096), dtype=torch.int32, pin_memory=True)
+                buf = self._bufs[i] = (t, t.numpy())
+            buf[1][:n] = arr
+            dev = torch.empty(max(n, 1), dtype=torch.int32, device=self.device)
+            stream = stream_ptr(self.device)
+            if n:
+                memcpy_h2d_async(dev.data_ptr(), buf[0].data_ptr(), 4 * n, stream)
+            if ev is None:
+                ev = self._events[i] = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.device))
         return dev[:n]
+
+
+_uploaders: dict = {}
+_uploaders_lock = threading.Lock()
+
+
+def uploader(device) -> PinnedUploader:
+    """The process-wide :class:`PinnedUploader` of ``device``."""
+    d = torch.device(device)
+    if d.type == "cuda" and d.index is None:
+        d = torch.device("cuda", torch.cuda.current_device())
+    with _uploaders_lock:
+        u = _uploaders.get(d)
+        if u is None:
+            u = _uploaders[d] = PinnedUploader(d)
+    return u
 
 
 _desc_cache: dict = {}

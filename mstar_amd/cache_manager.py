@@ -77,10 +77,6 @@ def _step_tensors(b: int, total_pages: int, decode: bool, device):
             buf[o_last:o_last + b], loc)
 
 
-class _PackBuffers(_lib.PinnedUploader):
-    """Uploads of the step metadata (one pinned staging pair per manager)."""
-
-
 class BatchedCacheManager:
     """Batched paged attention for the requests of one step (``cache_manager.py:56``)."""
 
@@ -115,7 +111,9 @@ class BatchedCacheManager:
         self._plan_states: dict[str, _PlanState] = cuda_graph_plan_states if cuda_graph_plan_states is not None else {}
         self._pre_planned_labels: set[str] = set()
         self._plan_done_event = None
-        self._pack = _PackBuffers(self.device)
+        # step metadata uploads: the device's shared pinned staging pair (managers
+        # are short-lived, one per batch in the reference engine)
+        self._pack = _lib.uploader(self.device)
         self._states_cache: dict = {}
         if alloc_manager.block_table is None:
             raise ValueError("the allocation manager needs a device (block table) for GPU packing")

@@ -98,3 +98,44 @@ def test_decode_wrapper_cuda_graph_replay(gpu):
         assert torch.equal(replay, eager)
         ref = A.paged_attention(q_static.cpu(), cache.cpu(), None, kv_indptr, kv_indices, last, causal=False)
         assert max_abs(replay, ref) < 2e-2
+
+
+def test_per_step_managers_with_gpu_behind_host(gpu):
+    """One manager per step (as the reference engine builds them) while the GPU runs
+    steps behind the host: every step's metadata upload must reach the GPU intact."""
+    hq, hkv, d, ps = 8, 2, 64, 16
+    cfg = KVCacheConfig(num_layers=1, num_kv_heads=hkv, head_dim=d, max_seq_len=4096, max_num_pages=400,
+                        page_size=ps, num_qo_heads=hq)
+    kv = torch.zeros(1, 400, 2, ps, hkv, d, dtype=torch.bfloat16, device=gpu)
+    mgr = PagedAllocationManager(cfg, kv, device=gpu)
+    bufs = WorkspaceBufferManager(64 << 20, gpu)
+    rids = [f"r{i}" for i in range(6)]
+    for r in rids:
+        mgr.add_request(r, ["main"])
+    g = torch.Generator().manual_seed(4)
+    schedule = [[20, 33, 1, 7, 64, 15]] + [[1] * 6] * 11
+    ins, outs = [], []
+    for seq_lens in schedule:
+        cm = BatchedCacheManager(rids, {r: "main" for r in rids}, kv, mgr, bufs, cfg, gpu)
+        cm.plan_attention(seq_lens, is_causal=True)
+        n = sum(seq_lens)
+        q = torch.randn(n, hq, d, generator=g).to(torch.bfloat16)
+        k = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+        v = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+        torch.cuda._sleep(1_000_000)  # keep the GPU behind: the host plans ahead
+        outs.append(cm.run_attention(q.to(gpu, non_blocking=True), k.to(gpu), v.to(gpu)))
+        ins.append((q, k, v))
+        cm.advance_seq_lens()
+    torch.cuda.synchronize()
+    hist = {r: ([], []) for r in rids}
+    for (q, k, v), out, seq_lens in zip(ins, outs, schedule):
+        off = 0
+        ref = torch.zeros(q.shape)
+        for r, sl in zip(rids, seq_lens):
+            hist[r][0].append(k[off:off + sl])
+            hist[r][1].append(v[off:off + sl])
+            if sl:
+                ref[off:off + sl], _ = A.attend(q[off:off + sl], torch.cat(hist[r][0]), torch.cat(hist[r][1]),
+                                                causal=True, sm_scale=d ** -0.5)
+            off += sl
+        assert max_abs(out, ref) < 2e-2
