@@ -489,49 +489,48 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
 #pragma unroll
   for (int i = 0; i < NS; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   const int64_t u0 = (int64_t)c0 * nkv + h;  // unit of chunk c: u0 + c * nkv
-  float M = kNegInf;
-#pragma unroll 8
-  for (int c = 0; c < nb; ++c) M = fmaxf(M, p.lse_part[(u0 + (int64_t)c * nkv) * kRows + col]);
-  float wsum = 0.f;
-  if (M != kNegInf) {
-    constexpr int U = 2;  // partials in flight per step
-    int c = 0;
-    for (; c + U <= nb; c += U) {
-      float w[U];
-      float4 o[U][NS];
+  // One pass: each group of U partials is loaded with its lse values at
+  // once (no separate max pass ahead of the loads), and the running sum is
+  // rescaled when a partial raises the running max.
+  float M = kNegInf, wsum = 0.f;
+  constexpr int U = D > 128 ? 2 : 4;  // partials in flight per step
+  for (int c = 0; c < nb; c += U) {
+    float w[U];
+    float4 o[U][NS];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < U; ++u) {
+      w[u] = kNegInf;
+      if (c + u < nb) {
         const int64_t unit = u0 + (int64_t)(c + u) * nkv;
         w[u] = p.lse_part[unit * kRows + col];
         const float* src = p.o_part + unit * kRows * D + 4 * lane;
 #pragma unroll
         for (int i = 0; i < NS; ++i) o[u][i] = *(const float4*)(src + 256 * i);
       }
+    }
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const float wgt = fast_exp2(w[u] - M);
-        wsum += wgt;
+    for (int u = 0; u < U; ++u) {
+      if (!(w[u] > kNegInf)) continue;  // past the end, or an empty partial
+      if (w[u] > M) {
+        const float sc = fast_exp2(M - w[u]);  // 0 while M is -inf
+        wsum *= sc;
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
-          acc[i].x += wgt * o[u][i].x;
-          acc[i].y += wgt * o[u][i].y;
-          acc[i].z += wgt * o[u][i].z;
-          acc[i].w += wgt * o[u][i].w;
+          acc[i].x *= sc;
+          acc[i].y *= sc;
+          acc[i].z *= sc;
+          acc[i].w *= sc;
         }
+        M = w[u];
       }
-    }
-    for (; c < nb; ++c) {
-      const int64_t unit = u0 + (int64_t)c * nkv;
-      const float wgt = fast_exp2(p.lse_part[unit * kRows + col] - M);
+      const float wgt = fast_exp2(w[u] - M);
       wsum += wgt;
-      const float* src = p.o_part + unit * kRows * D + 4 * lane;
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
-        const float4 o = *(const float4*)(src + 256 * i);
-        acc[i].x += wgt * o.x;
-        acc[i].y += wgt * o.y;
-        acc[i].z += wgt * o.z;
-        acc[i].w += wgt * o.w;
+        acc[i].x += wgt * o[u][i].x;
+        acc[i].y += wgt * o[u][i].y;
+        acc[i].z += wgt * o[u][i].z;
+        acc[i].w += wgt * o[u][i].w;
       }
     }
   }
