@@ -422,18 +422,31 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // Three register buffers: tile i is loaded three steps before it is stored
   constexpr int NB = 3;
   uint4 rr[NB][NL];
-  auto load_tile = [&](int t, uint4 (&r)[NL]) {
+  // A tile's loads in two parts: the page ids (LDS reads) and the global
+  // loads, so a step can read its page ids early and issue the loads later.
+  auto tile_pages = [&](int t, int (&pg)[NL]) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      // groups past the request's last page re-read its last group (masked, V zeroed)
+      const int gkey = uniform(min(t * KEYS + l_grp[i], key_cap));
+      pg[i] = lds_pages[gkey / ps - c0];
+    }
+  };
+  auto load_tile_at = [&](int t, const int (&pg)[NL], uint4 (&r)[NL]) {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       if (2 * HALF % THREADS == 0 || tid + i * THREADS < 2 * HALF) {
-        // groups past the request's last page re-read its last group (masked, V zeroed)
         const int gkey = uniform(min(t * KEYS + l_grp[i], key_cap));
-        const int pabs = gkey / ps;
-        const int page = uniform(lds_pages[pabs - c0]);
-        const uint8_t* base = kvb + (int64_t)page * p.page_stride * ESZ + (int64_t)(gkey - pabs * ps) * tok_bytes;
+        const int page = uniform(pg[i]);
+        const uint8_t* base = kvb + (int64_t)page * p.page_stride * ESZ + (int64_t)(gkey % ps) * tok_bytes;
         r[i] = *(const uint4*)(base + l_off[i]);
       }
     }
+  };
+  auto load_tile = [&](int t, uint4 (&r)[NL]) {
+    int pg[NL];
+    tile_pages(t, pg);
+    load_tile_at(t, pg, r);
   };
   auto store_tile = [&](int t, const uint4 (&r)[NL], int stage) {
 #pragma unroll
@@ -644,11 +657,13 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         // Tile T+1 goes into the stage tile T-2 used, which no wave reads in
         // this step; each group stores it (and issues the loads of tile T+4)
         // in its vector half, under the other group's MFMA work.
+        int pg4[NL];
+        tile_pages(min(T + 4, tl), pg4);
         if (grp_a) {
           store_tile(min(T + 1, tl), rr[(u + 2) % 3], (u + 2) % 3);
-          load_tile(min(T + 4, tl), rr[(u + 2) % 3]);
           sm_max(T - 1, sc);
           sm_exp(sc, pbk);
+          load_tile_at(min(T + 4, tl), pg4, rr[(u + 2) % 3]);
         }
         if constexpr (!VPRE) vfrag(u % 3, va);  // stage of tile T-1 = (ii-1) % 3 = u
         pv(va, pbk);               // tile T-1
@@ -656,7 +671,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         if constexpr (VPRE) vfrag((u + 1) % 3, va);
         if (!grp_a) {
           store_tile(min(T + 1, tl), rr[(u + 2) % 3], (u + 2) % 3);
-          load_tile(min(T + 4, tl), rr[(u + 2) % 3]);
+          load_tile_at(min(T + 4, tl), pg4, rr[(u + 2) % 3]);
           sm_max(T, sc);
           sm_exp(sc, pbk);
         }
