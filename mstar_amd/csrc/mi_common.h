@@ -54,23 +54,20 @@ MI_DEVICE float f16_to_f32(uint16_t h) { return (float)bitcast<_Float16>(h); }
 // float -> OCP fp8 e4m3fn (bias 7, no infinities, 0x7F/0xFF = NaN, max 448).
 // Round-to-nearest-even.  Magnitudes that round past 448 (>= 464) and NaN
 // map to NaN, matching torch's non-saturating float8_e4m3fn cast; callers
-// clamp to +-448 first.
+// clamp to +-448 first.  Branch-free: both the normal and the subnormal
+// result are formed and one is selected.  Normal range: adding 0x7ffff plus
+// the lowest kept mantissa bit rounds the 20 dropped bits to nearest-even on
+// the bit pattern, a carry moving into the exponent; (bits >> 20) is then
+// exponent:mantissa, and subtracting 120 << 3 rebiases 127 -> 7.
 MI_DEVICE uint8_t f32_to_e4m3fn(float x) {
   const uint32_t u = bitcast<uint32_t>(x);
   const uint32_t sign = (u >> 24) & 0x80u;
   const uint32_t a = u & 0x7fffffffu;
-  if (a >= 0x43e80000u) return (uint8_t)(sign | 0x7fu);  // >= 464.0 or NaN/inf
-  if (a < 0x3c800000u) {                                  // < 2^-6: subnormal grid 2^-9
-    const float q = __builtin_rintf(bitcast<float>(a) * 512.0f);  // exact scale, RNE
-    return (uint8_t)(sign | (uint32_t)q);                 // q == 8 encodes 2^-6
-  }
-  uint32_t e = (a >> 23) - 120u;  // rebias 127 -> 7, in [1, 15]
-  uint32_t m = (a >> 20) & 7u;
-  const uint32_t rem = a & 0xfffffu;
-  if (rem > 0x80000u || (rem == 0x80000u && (m & 1u))) {
-    if (++m == 8u) { m = 0u; ++e; }
-  }
-  return (uint8_t)(sign | (e << 3) | m);
+  const uint32_t nrm = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - (120u << 3);
+  // < 2^-6: subnormal grid 2^-9, exact scale then RNE; q == 8 encodes 2^-6.
+  const uint32_t sub = (uint32_t)__builtin_rintf(bitcast<float>(a) * 512.0f);
+  const uint32_t v = a < 0x3c800000u ? sub : nrm;
+  return (uint8_t)(sign | (a >= 0x43e80000u ? 0x7fu : v));  // >= 464.0 or NaN/inf
 }
 
 // ------------------------------------------------------------ type traits

@@ -175,8 +175,9 @@ MI_DEVICE void cache_store(uint8_t* dst, const uint32_t* w, float inv_scale) {
   }
 }
 
-// One thread: one 8-element group g of one token for kRopeHeads heads taken
-// from [q heads | k heads | v heads].  Groups g < rotary_dim/8 hold 4 pairs
+// One thread: one 8-element group g of one token for kRopeHeads q heads, or
+// for one k or one v head (the cache conversion, fp8 above all, is the long
+// part of a thread; one head each spreads it over more threads).  Groups g < rotary_dim/8 hold 4 pairs
 // (elements 4g.. and rotary_dim/2 + 4g.., or 8g.. interleaved); the others,
 // and every v group, are elements 8g .. 8g+7, copied unrotated.
 template <typename MT, int DST, bool INTERLEAVE>
@@ -184,20 +185,22 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams a) {
   constexpr int ESZ = DST == MI_FP8_E4M3 ? 1 : 2;
   const RopeParams& p = a.r;
   const int groups = a.head_dim >> 3, rgroups = p.rotary_dim >> 3, half = p.rotary_dim >> 1;
-  const int hq = p.num_qo_heads, hkv = p.num_kv_heads, nh = hq + 2 * hkv;
-  const int chunks = (nh + kRopeHeads - 1) / kRopeHeads;
+  const int hq = p.num_qo_heads, hkv = p.num_kv_heads;
+  const int qchunks = (hq + kRopeHeads - 1) / kRopeHeads, chunks = qchunks + 2 * hkv;
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t t = gid / (groups * chunks);
   if (t >= p.num_tokens) return;
   const int rem = (int)(gid - t * groups * chunks);
   const int chunk = rem / groups, g = rem - chunk * groups;
-  const int h0 = chunk * kRopeHeads;
+  const bool kvc = chunk >= qchunks;  // a k or v head: the one head hq + chunk - qchunks
+  const int h0 = kvc ? hq + chunk - qchunks : chunk * kRopeHeads;
+  const int hend = kvc ? h0 + 1 : min(h0 + kRopeHeads, hq);
   const bool rot = g < rgroups;
   // The token's cache row (K half, head 0), or null when it is not written.
   // (The index entries exist for t < num_append; the device count, read in
   // parallel, only trims that range.)
   uint8_t* crow = nullptr;
-  if (t < a.num_append && h0 + kRopeHeads > hq) {
+  if (t < a.num_append && kvc) {
     const bool real = !a.num_tokens_device || t < *a.num_tokens_device;
     const int64_t page = a.page_idx[t * a.idx_stride], slot = a.slot_idx[t * a.idx_stride];
     if (real && page >= 0 && page < a.max_pages && slot >= 0 && slot < a.page_size)
@@ -213,16 +216,29 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams a) {
 #pragma unroll
   for (int j = 0; j < kRopeHeads; ++j) {
     const int hh = h0 + j;
-    if (hh < hq) {
+    if (hh >= hend) {
+      live[j] = false;
+      src[j] = nullptr;
+    } else if (hh < hq) {
       live[j] = rot;
       src[j] = (uint16_t*)p.q + t * p.q_stride_tok + (int64_t)hh * p.q_stride_head;
     } else if (hh < hq + hkv) {
       live[j] = true;
       src[j] = (uint16_t*)p.k + t * p.k_stride_tok + (int64_t)(hh - hq) * p.k_stride_head;
     } else {
-      live[j] = hh < nh;
+      live[j] = true;
       src[j] = (uint16_t*)a.v + t * a.v_stride_tok + (int64_t)(hh - hq - hkv) * a.v_stride_head;
     }
+  }
+  // fp8 cache: the heads' reciprocal scales, loaded beside the rows (every
+  // k and v head has a scale, whatever the page lookup finds).
+  float isc[kRopeHeads];
+#pragma unroll
+  for (int j = 0; j < kRopeHeads; ++j) {
+    const int hh = h0 + j;
+    isc[j] = 1.f;
+    if (DST == MI_FP8_E4M3 && hh >= hq && hh < hend)
+      isc[j] = 1.0f / (hh < hq + hkv ? a.k_scale[hh - hq] : a.v_scale[hh - hq - hkv]);
   }
   float c[4] = {}, s[4] = {};
   if (rot && h0 < hq + hkv) rope_cos_sin(p, t, 4 * g, c, s);
@@ -245,8 +261,7 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams a) {
     if (hh >= hq + hkv) {  // v head: unrotated, 8 elements
       if (!crow) continue;
       const int vh = hh - hq - hkv;
-      const float iv = DST == MI_FP8_E4M3 ? 1.0f / a.v_scale[vh] : 1.f;
-      cache_store<MT, DST, 4>(crow + (a.kv_stride + vh * a.head_stride + 8 * g) * ESZ, w[j], iv);
+      cache_store<MT, DST, 4>(crow + (a.kv_stride + vh * a.head_stride + 8 * g) * ESZ, w[j], isc[j]);
       continue;
     }
     const bool is_k = hh >= hq;
@@ -269,10 +284,9 @@ __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams a) {
     }
     if (is_k && crow) {
       const int kh = hh - hq;
-      const float ik = DST == MI_FP8_E4M3 ? 1.0f / a.k_scale[kh] : 1.f;
       uint8_t* row = crow + (int64_t)kh * a.head_stride * ESZ;
-      cache_store<MT, DST, 2>(row + e0 * ESZ, w[j], ik);
-      cache_store<MT, DST, 2>(row + e1 * ESZ, w[j] + 2, ik);
+      cache_store<MT, DST, 2>(row + e0 * ESZ, w[j], isc[j]);
+      cache_store<MT, DST, 2>(row + e1 * ESZ, w[j] + 2, isc[j]);
     }
   }
 }
@@ -452,7 +466,7 @@ extern "C" int mi_rope_append(void* q, int64_t q_stride_token, int64_t q_stride_
   a.head_dim = d;
   a.page_size = kv->page_size;
   a.keep_k = keep_k ? 1 : 0;
-  const int64_t chunks = (num_qo_heads + 2 * hkv + kRopeHeads - 1) / kRopeHeads;
+  const int64_t chunks = (num_qo_heads + kRopeHeads - 1) / kRopeHeads + 2 * hkv;
   const int64_t threads = (int64_t)num_tokens * chunks * (d / 8);
   if ((threads + 255) / 256 > INT32_MAX) return MI_ERR_INVALID;
   const int grid = (int)((threads + 255) / 256);

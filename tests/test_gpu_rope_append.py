@@ -59,7 +59,18 @@ def _cache(pool, ps, hkv, d, dtype, gpu, seed):
 
 @pytest.mark.parametrize("dtype,cdt,d,rd,interleave,llama31,keep_k,idx_stride", CASES)
 def test_rope_append_matches_rope_then_append(gpu, dtype, cdt, d, rd, interleave, llama31, keep_k, idx_stride):
-    t, hq, hkv, pool, ps = 203, 12, 3, 64, 16
+    _check_rope_append(gpu, dtype, cdt, d, rd, interleave, llama31, keep_k, idx_stride, 12, 3)
+
+
+@pytest.mark.parametrize("cdt", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("hq,hkv", [(6, 3), (5, 1), (1, 2)])
+def test_rope_append_partial_q_head_groups(gpu, cdt, hq, hkv):
+    """q head counts that leave the last group of four q heads partly empty."""
+    _check_rope_append(gpu, torch.bfloat16, cdt, 128, 128, False, None, True, 1, hq, hkv)
+
+
+def _check_rope_append(gpu, dtype, cdt, d, rd, interleave, llama31, keep_k, idx_stride, hq, hkv):
+    t, pool, ps = 203, 64, 16
     n_append, n_dev = 190, 170  # tokens >= 170 are graph padding: rotated, not written
     q, k, v, pos, idx = _inputs(d + rd, t, hq, hkv, d, dtype, pool, ps, idx_stride, gpu)
     page_idx, slot_ptr = idx[0], idx[1]
