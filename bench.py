@@ -561,7 +561,7 @@ def bench_prefill(args, dev) -> dict:
     for kvl, qo in zip(bt.kv_len.tolist(), bt.new_len.tolist()):
         if qo * g_ <= 16:
             short_bytes += kvl * s.num_kv_heads * s.head_dim * 2 * 2 + qo * s.num_qo_heads * s.head_dim * 2 * 2
-    return {
+    res = {
         "metric": "ragged prefill+decode attn tokens/s + prefill MFMA TFLOP/s, 1 MI355X",
         "value": ntok / wall,
         "unit": "tokens/s",
@@ -596,6 +596,43 @@ def bench_prefill(args, dev) -> dict:
                                  "GBps": short_bytes / (float(short_ms.mean()) * 1e-3) / 1e9},
         },
     }
+    res["prefill_head_dim_256"] = bench_prefill_d256(dev, args.steps)
+    return res
+
+
+def bench_prefill_d256(dev, steps: int) -> dict:
+    """The prefill kernel at head_dim 256 (its own register layout): 8 requests of
+    2048 new tokens over 4096..7680-token contexts, 16 q / 2 kv heads, page 16,
+    bf16, causal; HIP events around ``run`` (short-query part empty)."""
+    from mstar_amd.paged_attention import PagedPrefillWrapper
+
+    hq, hkv, d, ps = 16, 2, 256, 16
+    kv_lens = [4096 + 512 * i for i in range(8)]
+    new = [2048] * 8
+    pages = [-(-n // ps) for n in kv_lens]
+    pool = sum(pages) + 8
+    perm = np.random.default_rng(0).permutation(pool)
+    kv_indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    kv_indices = perm[: kv_indptr[-1]].astype(np.int32)
+    last = np.array([n - (p - 1) * ps for n, p in zip(kv_lens, pages)], np.int32)
+    qo = np.concatenate([[0], np.cumsum(new)]).astype(np.int32)
+    g = torch.Generator(device=dev).manual_seed(5)
+    cache = torch.randn(pool, 2, ps, hkv, d, device=dev, generator=g).to(torch.bfloat16)
+    q = torch.randn(int(qo[-1]), hq, d, device=dev, generator=g).to(torch.bfloat16)
+    w = PagedPrefillWrapper(torch.empty(512 << 20, dtype=torch.uint8, device=dev), hq, hkv, d, ps, device=dev)
+    w.plan(*(torch.from_numpy(a) for a in (qo, kv_indptr, kv_indices, last)), causal=True)
+    for _ in range(2):
+        w.run(q, cache)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        w.run(q, cache)
+        b.record()
+    torch.cuda.synchronize()
+    us = float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3
+    flops = sum(4 * hq * d * (kl - n + t + 1) for kl, n in zip(kv_lens, new) for t in range(n))
+    return {"kernel": "prefill_kernel<BF16, false, 256>", "us": us, "algorithmic_flops": flops,
+            "TFLOPs": flops / us / 1e6, "frac": flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS}
 
 
 def _prefill_split(w, q, layer, events):

@@ -35,8 +35,12 @@ namespace mi {
 
 // Wavefronts per prefill workgroup (32 rows each): 8 (two per SIMD) while
 // the per-wave state fits 256 registers, 4 for head_dim 256.
-constexpr int pf_waves(int head_dim) { return head_dim > 128 ? 4 : 8; }
-constexpr int pf_rows(int head_dim) { return 32 * pf_waves(head_dim); }  // (token, q-head) rows per workgroup
+// Eight wavefronts (two per SIMD, in ping-pong) with two 16-row groups each;
+// head_dim 256 keeps its accumulators within a two-wavefront register share
+// with one 16-row group per wavefront.
+constexpr int pf_waves(int) { return 8; }
+constexpr int pf_rg(int head_dim) { return head_dim > 128 ? 1 : 2; }  // 16-row groups per wavefront
+constexpr int pf_rows(int head_dim) { return 16 * pf_rg(head_dim) * pf_waves(head_dim); }  // (token, q-head) rows per workgroup
 constexpr int kPfKeys = 32;                // keys per K/V tile
 constexpr int kPfPageCap = 2048;           // page ids staged in LDS at a time
 constexpr int kShortRows = 16;  // qo_len * group <= 16 -> decode kernel
@@ -320,6 +324,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   using C = PrefillCfg<MT, FP8, D>;
   constexpr int KS = D / 32, VW = D / 16, KEYS = C::KEYS, RSK = C::RSK, RSV = C::RSV, ESZ = C::ESZ, CPR = C::CPR;
   constexpr int THREADS = C::THREADS, NL = C::NL, HALF = C::HALF, STAGE = C::STAGE;
+  constexpr int RG = pf_rg(D), WROWS = 16 * RG;  // 16-row groups and rows per wavefront
   constexpr int LCH = FP8 ? 32 : 16;  // LDS bytes per loaded chunk
   constexpr float kNegInf = -__builtin_inff();
   __shared__ __attribute__((aligned(16))) uint8_t lds[3 * STAGE];
@@ -365,12 +370,12 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   const int kv_len = (np - 1) * ps + p.last_page_len[b];
   const int rows_total = qo_len * G;
 
-  // ---- this lane's two query rows (one per 16-row group)
-  uint4 qf[2][KS];
-  int lim[2];
+  // ---- this lane's query rows (one per 16-row group)
+  uint4 qf[RG][KS];
+  int lim[RG];
 #pragma unroll
-  for (int rg = 0; rg < 2; ++rg) {
-    const int n = row0 + 32 * wave + 16 * rg + col;
+  for (int rg = 0; rg < RG; ++rg) {
+    const int n = row0 + WROWS * wave + 16 * rg + col;
     const int tok = n / G, g = n - tok * G;
     const bool valid = n < rows_total;
     const int l = p.causal ? (kv_len - qo_len + tok) : (kv_len - 1);
@@ -476,9 +481,9 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     }
   };
 
-  f32x4 acc[2][VW];
+  f32x4 acc[RG][VW];
 #pragma unroll
-  for (int rg = 0; rg < 2; ++rg)
+  for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
     for (int jj = 0; jj < VW; ++jj) acc[rg][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
   // Running max in raw-score units.  It is raised only when a tile's max
@@ -487,8 +492,13 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // is skipped on almost every tile.
   constexpr float kLazy = 8.f;
   const float lazy_raw = kLazy / sl2;
-  float m_run[2] = {kNegInf, kNegInf}, l_run[2] = {0.f, 0.f};
-  float thr[2] = {kNegInf, kNegInf};  // m_run + lazy_raw
+  float m_run[RG], l_run[RG], thr[RG];  // thr = m_run + lazy_raw
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    m_run[rg] = kNegInf;
+    l_run[rg] = 0.f;
+    thr[rg] = kNegInf;
+  }
 
   // first tile that reaches past some row's limit: (t+1)*KEYS > mask_from
   const int t_mask = mask_from > 0 ? mask_from / KEYS : 0;
@@ -499,7 +509,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // index i of lane group grp stands for key 4*grp+i (i < 4) or 16+4*grp+i-4
   // (i >= 4): exactly the keys whose scores that lane holds, so P^T needs no
   // shuffle.
-  auto qk = [&](int stage, f32x4 (&s)[2][2]) {
+  auto qk = [&](int stage, f32x4 (&s)[RG][2]) {
     const uint8_t* sk = lds + stage * STAGE;
     uint4 a[2][KS];
 #pragma unroll
@@ -507,28 +517,36 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
 #pragma unroll
       for (int st = 0; st < KS; ++st) a[js][st] = *(const uint4*)(sk + (16 * js + col) * RSK + (8 * grp + 32 * st) * 2);
 #pragma unroll
-    for (int js = 0; js < 2; ++js) {
-      s[0][js] = f32x4{0.f, 0.f, 0.f, 0.f};
-      s[1][js] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+      for (int js = 0; js < 2; ++js) s[rg][js] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < KS; ++st)
 #pragma unroll
-      for (int js = 0; js < 2; ++js) {
-        s[0][js] = MT::mma_16x16x32(a[js][st], qf[0][st], s[0][js]);
-        s[1][js] = MT::mma_16x16x32(a[js][st], qf[1][st], s[1][js]);
+      for (int js = 0; js < 2; ++js)
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) s[rg][js] = MT::mma_16x16x32(a[js][st], qf[rg][st], s[rg][js]);
+    if constexpr (D <= 128) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * KS, 0);  // all K fragment reads first
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * RG * KS, 0);  // then the MFMAs
+    } else {  // head_dim 256: reads of slice st+1 ahead of the MFMAs of slice st (registers)
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int st = 1; st < KS; ++st) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * RG, 0);
       }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * KS, 0);  // all K fragment reads first
-    __builtin_amdgcn_sched_group_barrier(0x008, 4 * KS, 0);  // then the MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * RG, 0);
+    }
   };
   // Softmax in two parts: sm_max masks (tail tiles only), takes the row max
   // and raises the running max when needed (a rare branch); sm_exp forms
   // the probabilities and their row sums.
-  auto sm_max = [&](int t, f32x4 (&s)[2][2]) {
+  auto sm_max = [&](int t, f32x4 (&s)[RG][2]) {
     const int kb = t * KEYS;
     if (t >= t_mask) {  // wave-uniform: only the tiles that reach past some row's limit
 #pragma unroll
-      for (int rg = 0; rg < 2; ++rg)
+      for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
         for (int js = 0; js < 2; ++js)
 #pragma unroll
@@ -537,21 +555,21 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     }
     // A row's max exceeds the threshold iff one of its four lanes' maxima
     // does, so the cross-lane row max is only needed on the rare branch.
-    float ml[2];
-    bool need[2];
+    float ml[RG];
+    bool any_need = false;
 #pragma unroll
-    for (int rg = 0; rg < 2; ++rg) {
+    for (int rg = 0; rg < RG; ++rg) {
       float m = kNegInf;
 #pragma unroll
       for (int js = 0; js < 2; ++js)
 #pragma unroll
         for (int r = 0; r < 4; ++r) m = fmaxf(m, s[rg][js][r]);
       ml[rg] = m;
-      need[rg] = m > thr[rg];
+      any_need |= m > thr[rg];
     }
-    if (__builtin_amdgcn_ballot_w64(need[0] || need[1])) {
+    if (__builtin_amdgcn_ballot_w64(any_need)) {
 #pragma unroll
-      for (int rg = 0; rg < 2; ++rg) {
+      for (int rg = 0; rg < RG; ++rg) {
         const float mt = rows4_max(ml[rg]);
         const bool grow = mt > thr[rg];
         const float alpha = grow ? fast_exp2((m_run[rg] - mt) * sl2) : 1.f;
@@ -565,9 +583,9 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       }
     }
   };
-  auto sm_exp = [&](const f32x4 (&s)[2][2], uint4 (&pb)[2]) {
+  auto sm_exp = [&](const f32x4 (&s)[RG][2], uint4 (&pb)[RG]) {
 #pragma unroll
-    for (int rg = 0; rg < 2; ++rg) {
+    for (int rg = 0; rg < RG; ++rg) {
       const float moff = m_run[rg] == kNegInf ? 0.f : -m_run[rg] * sl2;
       float pr[2][4];
 #pragma unroll
@@ -599,11 +617,19 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       a[jj] = make_uint4(a0.x, a0.y, a1.x, a1.y);
     }
   };
-  auto pv = [&](const uint4 (&a)[VW], const uint4 (&pb)[2]) {
+  auto pv = [&](const uint4 (&a)[VW], const uint4 (&pb)[RG]) {
 #pragma unroll
-    for (int jj = 0; jj < VW; ++jj) {
-      acc[0][jj] = MT::mma_16x16x32(a[jj], pb[0], acc[0][jj]);
-      acc[1][jj] = MT::mma_16x16x32(a[jj], pb[1], acc[1][jj]);
+    for (int jj = 0; jj < VW; ++jj)
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) acc[rg][jj] = MT::mma_16x16x32(a[jj], pb[rg], acc[rg][jj]);
+    if constexpr (!VPRE) {  // fragments read just before: the reads of tile jj+1 ahead of its MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int jj = 1; jj < VW; ++jj) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, RG, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, RG, 0);
     }
   };
   // Ping-pong: the two wavefronts that share a SIMD (one of waves {0,2,5,7},
@@ -634,8 +660,8 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     store_tile(t0, rr[0], 0);
     load_tile(min(t0 + 3, tl), rr[0]);
     __syncthreads();
-    f32x4 sc[2][2];
-    uint4 pbk[2];
+    f32x4 sc[RG][2];
+    uint4 pbk[RG];
     uint4 va[VW];
     // step 0: scores and V^T fragments of tile t0; group B also its softmax
     qk(0, sc);
@@ -689,10 +715,10 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
 
   // ---- epilogue: lane holds dims 16*jj + 4*grp + r of its row
 #pragma unroll
-  for (int rg = 0; rg < 2; ++rg) {
+  for (int rg = 0; rg < RG; ++rg) {
     const float l_tot = rows4_sum(l_run[rg]);
     const float inv = l_tot > 0.f ? vscale / l_tot : 0.f;
-    const int n = row0 + 32 * wave + 16 * rg + col;
+    const int n = row0 + WROWS * wave + 16 * rg + col;
     if (n >= rows_total) continue;
     const int tok = n / G, g = n - tok * G;
     uint16_t* orow = (uint16_t*)p.out + (int64_t)(qo_start + tok) * p.out_stride_tok +
