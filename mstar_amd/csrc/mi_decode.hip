@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   constexpr int KS = D / 32;  // MFMA k-steps over head_dim for S
   constexpr int VW = D / 16;  // V elements per lane per row == output d-tiles
   constexpr int ESZ = FP8 ? 1 : 2;
-  constexpr int KRS = D * 2 + 16;  // LDS row stride of the K transpose buffer (padded)
+  constexpr int KRS = D * 2 + 32;  // LDS row stride of the K transpose buffer (8-bank step: conflict-free fragment reads)
   constexpr int NS = VW / 4;       // float4 groups per lane per output row segment
   constexpr float kNegInf = -__builtin_inff();
   // LDS: during the tile loop, per-wave K staging (rows arrive as whole
