@@ -597,7 +597,34 @@ def bench_prefill(args, dev) -> dict:
         },
     }
     res["prefill_head_dim_256"] = bench_prefill_d256(dev, args.steps)
+    res["prefill_fp8_kv"] = bench_prefill_fp8(w, q, layer, s, dev, args.steps, long_f)
     return res
+
+
+def _run_us(fn, steps: int) -> float:
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3
+
+
+def bench_prefill_fp8(w, q, layer, s, dev, steps: int, long_flops: int) -> dict:
+    """The same planned c4 batch over an fp8-e4m3 copy of the pool (per-head
+    scales, the fill_pool quantisation): ``run`` timed whole (short-query
+    decode part + prefill tiles) for the bf16 and the fp8 pool."""
+    kv8 = torch.empty((1,) + tuple(layer.shape), dtype=torch.float8_e4m3fn, device=dev)
+    scales = fill_pool(kv8, s, dev)
+    ks, vs = scales[0, 0].contiguous(), scales[0, 1].contiguous()
+    l8 = kv8[0]
+    for _ in range(2):
+        w.run(q, l8, k_scale=ks, v_scale=vs)
+    bf = _run_us(lambda: w.run(q, layer), steps)
+    f8 = _run_us(lambda: w.run(q, l8, k_scale=ks, v_scale=vs), steps)
+    return {"what": "run() of the planned c4 batch, bf16 pool vs fp8-e4m3 pool (in-register dequantisation)",
+            "run_us_bf16": bf, "run_us_fp8": f8, "prefill_part_flops": long_flops}
 
 
 def bench_prefill_d256(dev, steps: int) -> dict:
