@@ -683,21 +683,28 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         // in its vector half, under the other group's MFMA work.
         int pg4[NL];
         tile_pages(min(T + 4, tl), pg4);
+        // Each group's vector half runs at raised wave priority, so its softmax
+        // issues ahead of the partner's MFMA stream on the shared SIMD
+        // (c4 583 -> 580 us, head_dim 256 1794 -> 1747 us).
         if (grp_a) {
+          __builtin_amdgcn_s_setprio(1);
           store_tile(min(T + 1, tl), rr[(u + 2) % 3], (u + 2) % 3);
           sm_max(T - 1, sc);
           sm_exp(sc, pbk);
           load_tile_at(min(T + 4, tl), pg4, rr[(u + 2) % 3]);
+          __builtin_amdgcn_s_setprio(0);
         }
         if constexpr (!VPRE) vfrag(u % 3, va);  // stage of tile T-1 = (ii-1) % 3 = u
         pv(va, pbk);               // tile T-1
         qk((u + 1) % 3, sc);       // stage of tile T = ii % 3
         if constexpr (VPRE) vfrag((u + 1) % 3, va);
         if (!grp_a) {
+          __builtin_amdgcn_s_setprio(1);
           store_tile(min(T + 1, tl), rr[(u + 2) % 3], (u + 2) % 3);
           load_tile_at(min(T + 4, tl), pg4, rr[(u + 2) % 3]);
           sm_max(T, sc);
           sm_exp(sc, pbk);
+          __builtin_amdgcn_s_setprio(0);
         }
         __syncthreads();
       }
