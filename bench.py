@@ -335,9 +335,10 @@ def bench_decode(args, dev) -> dict:
         },
     }
     pos_now = np.array([cm._get_state(r).seq_len for r in rids])
-    res["rope"] = bench_rope(q, k, pos_now, args.steps)
-    res["rope_append"] = bench_rope_append(cm, q, k, v, pos_now, args.steps)
-    res["kv_transfer"] = bench_transfer(kv, args.steps)
+    if not args.no_extra:
+        res["rope"] = bench_rope(q, k, pos_now, args.steps)
+        res["rope_append"] = bench_rope_append(cm, q, k, v, pos_now, args.steps)
+        res["kv_transfer"] = bench_transfer(kv, args.steps)
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
         res["cpu_baseline"] = cpu_baseline(bt, kv, q, k, v, cm.kv_scales)
@@ -596,8 +597,9 @@ def bench_prefill(args, dev) -> dict:
                                  "GBps": short_bytes / (float(short_ms.mean()) * 1e-3) / 1e9},
         },
     }
-    res["prefill_head_dim_256"] = bench_prefill_d256(dev, args.steps)
-    res["prefill_fp8_kv"] = bench_prefill_fp8(w, q, layer, s, dev, args.steps, long_f)
+    if not args.no_extra:
+        res["prefill_head_dim_256"] = bench_prefill_d256(dev, args.steps)
+        res["prefill_fp8_kv"] = bench_prefill_fp8(w, q, layer, s, dev, args.steps, long_f)
     return res
 
 
@@ -686,6 +688,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c3", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="only the step loop: skip the side measurements (RoPE, KV transfer, "
+                         "head_dim 256 and fp8-pool prefill), e.g. for counter runs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 1 GiB (3x): the reference point that scales "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes")

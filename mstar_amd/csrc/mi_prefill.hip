@@ -694,9 +694,11 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
           load_tile_at(min(T + 4, tl), pg4, rr[(u + 2) % 3]);
           __builtin_amdgcn_s_setprio(0);
         }
+        // scores of tile T first (group B's softmax waits on them), then P.V of
+        // tile T-1; V^T fragments of tile T replace those of T-1 after it
+        qk((u + 1) % 3, sc);       // stage of tile T = ii % 3
         if constexpr (!VPRE) vfrag(u % 3, va);  // stage of tile T-1 = (ii-1) % 3 = u
         pv(va, pbk);               // tile T-1
-        qk((u + 1) % 3, sc);       // stage of tile T = ii % 3
         if constexpr (VPRE) vfrag((u + 1) % 3, va);
         if (!grp_a) {
           __builtin_amdgcn_s_setprio(1);
