@@ -172,6 +172,34 @@ int mi_decode_merge(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
                     int64_t out_stride_head, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Decode without a caller workspace.  No counterpart in the reference: this
+ * entry point is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * mi_decode_noalloc = mi_decode_plan(qo_indptr, kv_indptr, kv_indices,
+ * last_page_len, batch, kv->page_size, num_qo_heads, kv->num_kv_heads,
+ * kv->head_dim, kv_locations, ...) followed by mi_decode_run on the same
+ * stream, with the plan and the split-KV partials kept in a static device
+ * buffer the library holds on every GPU it runs on (MI_NOALLOC_SCRATCH_BYTES
+ * per device, until the process ends) instead of a workspace.  Outputs and
+ * kv_locations equal those of the two calls given a workspace of
+ * MI_NOALLOC_SCRATCH_BYTES bytes.  Limit: the buffer must hold batch + 1
+ * split-KV items of partials (4 * num_kv_heads * 16 * (head_dim + 1) bytes
+ * each, plus the plan's header and offsets; for 4 kv heads and head_dim 128
+ * a batch of up to about 2000 requests); a larger batch returns
+ * MI_ERR_WORKSPACE before anything is launched.  The stream must belong to
+ * the current device.  All calls on one GPU share its buffer, so calls that
+ * overlap on one GPU (two streams, or two threads without ordering between
+ * them) race.  Allocates nothing.
+ * ------------------------------------------------------------------------ */
+#define MI_NOALLOC_SCRATCH_BYTES (64LL << 20)
+int mi_decode_noalloc(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                      const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                      const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
+                      int32_t num_qo_heads, int32_t causal, float sm_scale, void* out,
+                      int64_t out_stride_token, int64_t out_stride_head, int64_t* kv_locations,
+                      void* stream);
+
+/* ------------------------------------------------------------------------
  * P5 — paged KV append.
  * Replaces FlashInferPrefillWrapper.set_kv_cache / FlashInferDecodeWrapper.set_kv_cache
  * (mstar/utils/flashinfer_utils.py:271-288, 467-484):

@@ -103,6 +103,11 @@ SIGNATURES = {
         [_P, _I32, _I64, _I64, ctypes.POINTER(MiPagedKV), _P, _P, _P, _P, _I32, _I32, _I32, _F32,
          _P, _I64, _P, _I64, _I64, _P],
     ),
+    "mi_decode_noalloc": (
+        ctypes.c_int,
+        [_P, _I32, _I64, _I64, ctypes.POINTER(MiPagedKV), _P, _P, _P, _P, _I32, _I32, _I32, _F32,
+         _P, _I64, _I64, _P, _P],
+    ),
     "mi_kv_append": (
         ctypes.c_int,
         [ctypes.POINTER(MiPagedKV), _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _P, _I64, _I32, _P, _P],

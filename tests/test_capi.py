@@ -187,3 +187,19 @@ def test_transfer_arguments_are_checked(L):
     assert L.mi_kv_copy_tokens(good, good, p, p, None, None, -1, 0, 1, None) == MI_ERR_INVALID
     assert L.mi_kv_copy_tokens(good, good, p, p, p, None, 1, 0, 1, None) == MI_ERR_INVALID
     assert L.mi_kv_wire_pack(good, p, p, None, None, 1, 0, 1, p, 64, None) == MI_ERR_INVALID
+
+
+def test_noalloc_decode_rejects_oversized_batch_on_the_host(L):
+    """mi_decode_noalloc checks the batch against its fixed device buffer before any HIP call."""
+    d = _lib.MiPagedKV()
+    d.data, d.dtype, d.page_size, d.num_kv_heads, d.head_dim = 4096, 0, 16, 4, 128
+    buf = (ctypes.c_int32 * 8)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    MI_ERR_WORKSPACE = -3
+    # about 33 KB of partials per split-KV item at 4 kv heads x head_dim 128: 4000 + 1 items exceed 64 MiB
+    assert L.mi_decode_noalloc(p, 0, 4096, 128, ctypes.byref(d), None, p, p, p, 4000, 32, 0, 0.1, p, 4096, 128,
+                               None, None) == MI_ERR_WORKSPACE
+    assert L.mi_decode_noalloc(p, 0, 4096, 128, None, None, p, p, p, 4, 32, 0, 0.1, p, 4096, 128, None,
+                               None) == MI_ERR_INVALID
+    assert L.mi_decode_noalloc(p, 0, 4096, 128, ctypes.byref(d), None, p, p, p, 0, 32, 0, 0.1, p, 4096, 128, None,
+                               None) == 0
