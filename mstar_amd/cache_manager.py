@@ -157,7 +157,8 @@ class BatchedCacheManager:
             return
         self._plan_attention_impl(seq_lens, dtype, is_causal, write_store, effective)
 
-    def _alloc_entries(self, entries: list[tuple[str, str]], seq_lens, states=None) -> np.ndarray:
+    def _alloc_entries(self, entries: list[tuple[str, str]], seq_lens, states=None,
+                       generation: int | None = None) -> np.ndarray:
         """FIFO allocation in batch order (``cache_manager.py:278-285``) and the pack
         kernel's input: per entry ``[slot | seq_len | new_len | num_pages | pages
         already on the device]``, followed by the pages not yet on the device.
@@ -167,10 +168,11 @@ class BatchedCacheManager:
         if len(seq_lens) != n:
             raise ValueError(f"{len(seq_lens)} seq_lens for {n} requests")
         if states is None:
+            generation = self.alloc_manager.state_generation
             states = [self._get_state(rid, label) for rid, label in entries]
         seq = np.array([st.seq_len for st in states], dtype=np.int64)
         sl = np.asarray(seq_lens, dtype=np.int64).reshape(n)
-        self.alloc_manager.alloc_batch(entries, states, seq + sl)
+        self.alloc_manager.alloc_batch(entries, states, seq + sl, generation)
         slots, npg, old, new_pages = self.alloc_manager.block_table.prepare_meta(states)
         meta = np.empty((5, n), dtype=np.int32)
         meta[0] = slots
@@ -180,18 +182,20 @@ class BatchedCacheManager:
         meta[4] = old
         return np.concatenate([meta.reshape(-1), new_pages])
 
-    def _label_states(self, label: str) -> tuple[list[tuple[str, str]], list[KVRequestState]]:
-        """Entries ``(rid, label)`` of every request and their state objects, kept
-        while the request list and the allocation manager's states are unchanged."""
+    def _label_states(self, label: str) -> tuple[list[tuple[str, str]], list[KVRequestState], int]:
+        """Entries ``(rid, label)`` of every request, their state objects and the
+        allocation manager's ``state_generation`` they were read at; kept while
+        the request list and the allocation manager's states are unchanged."""
         am = self.alloc_manager
         key = tuple(self.request_ids)
         c = self._states_cache.get(label)
-        if c is not None and c[0] == am.state_generation and c[1] == key:
-            return c[2], c[3]
+        gen = am.state_generation
+        if c is not None and c[0] == gen and c[1] == key:
+            return c[2], c[3], gen
         entries = [(rid, label) for rid in key]
         states = [am.get_state(rid, label) for rid in key]
-        self._states_cache[label] = (am.state_generation, key, entries, states)
-        return entries, states
+        self._states_cache[label] = (gen, key, entries, states)
+        return entries, states, gen
 
     def _launch_pack(self, meta: np.ndarray, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=None) -> None:
         """One upload of the step's metadata + new pages, one pack kernel; with
@@ -224,8 +228,8 @@ class BatchedCacheManager:
         cfg = self.kv_cache_config
         ps_ = cfg.page_size
         b = len(self.request_ids)
-        entries, states = self._label_states(label)
-        meta = self._alloc_entries(entries, seq_lens, states)
+        entries, states, gen = self._label_states(label)
+        meta = self._alloc_entries(entries, seq_lens, states, gen)
         total_pages = int(meta[3 * b:4 * b].sum())
         new_lens = meta[2 * b:3 * b]
         is_decode = bool((new_lens == 1).all())
@@ -543,7 +547,7 @@ class BatchedCacheManager:
         if len(labels) == 1 and pos_id_ns is None:  # one label, default advance: one pass over the states
             label = labels.pop()
             ps = self._plan_states[label]
-            _, states = self._label_states(label)
+            _, states, _ = self._label_states(label)
             adv = ps.custom_pos_advance if ps.custom_pos_advance is not None else ps.seq_lens
             for st, n, a in zip(states, ps.seq_lens, adv):
                 st.seq_len += n

@@ -35,8 +35,6 @@
 //           is why an item spans 4 wavefronts' worth of pages.
 //   merge : log-sum-exp merge of the item partials of split requests, in the
 //           same register-order layout (whole-cache-line loads and stores).
-#include <stdlib.h>
-
 #include "mi_common.h"
 #include "mi_internal.h"
 #include "mi_plan.h"
@@ -51,20 +49,11 @@ constexpr int kMinChunkTokens = 1024;  // never split a request finer than this 
 // longest-first work order the drain tail stays short while few requests
 // need partials (measured on c3: 4096 -> 545 us, 8192 -> 558 us,
 // 16384 -> 586 us).
-// MSTAR_DECODE_TARGET_UNITS overrides it for tuning sweeps (read once per
-// process).
-static int32_t decode_target_units() {
-  static const int32_t units = [] {
-    const char* e = getenv("MSTAR_DECODE_TARGET_UNITS");
-    int v = e ? atoi(e) : 4096;
-    return v < 64 ? 64 : v;
-  }();
-  return units;
-}
+constexpr int32_t kDecodeTargetUnits = 4096;
 
 SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t ws_avail) {
   SplitLayout L;
-  int32_t target = decode_target_units() / (4 * (nkv > 0 ? nkv : 1));  // 4 waves per item
+  int32_t target = kDecodeTargetUnits / (4 * (nkv > 0 ? nkv : 1));  // 4 waves per item
   if (target < 16) target = 16;
   int64_t max_chunks = (int64_t)target + batch;
   if (ws_avail >= 0) {  // fewer, longer chunks when the caller's workspace is smaller

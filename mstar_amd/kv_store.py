@@ -109,6 +109,14 @@ class KVRequestState:
     """Per-request, per-label KV state (``kv_store.py:111-127``).
 
     ``slot`` is this state's row in the :class:`DeviceBlockTable` (-1: none yet).
+
+    Page-list contract (what the reference's code paths do): ``page_indices``
+    only grows by ``append``/``extend``, or is replaced by a new list object.
+    The block table sends a grown list's new tail and a replaced list whole;
+    it also resends the whole list when the first page or the page last synced
+    no longer sits where it was, which catches edits in place of those entries
+    (``page_indices[:] = ...``).  Other in-place edits must be followed by
+    :meth:`pages_changed`.
     """
 
     page_indices: list[int] = field(default_factory=list)
@@ -119,6 +127,12 @@ class KVRequestState:
     slot: int = -1
     _dev_list: object = field(default=None, repr=False, compare=False)
     _dev_len: int = field(default=0, repr=False, compare=False)
+    _dev_ends: tuple = field(default=(-1, -1), repr=False, compare=False)
+
+    def pages_changed(self) -> None:
+        """Mark ``page_indices`` as edited in place: the next sync resends all of it."""
+        self._dev_list = None
+        self._dev_len = 0
 
 
 class AllocationFailedError(RuntimeError):
@@ -158,10 +172,22 @@ class DeviceBlockTable:
         return self.table.shape[0]
 
     def _grow(self) -> None:
+        """Double the table.  Pack and update kernels on any stream may still
+        read or write the old table: the device is drained before the copy and
+        after it, so the copy sees every earlier write and the old block is
+        not reused before the copy has read it.  Growth only happens when
+        more states are live than the table has rows (it starts at
+        ``max_slots``), never under graph capture (planning is not captured)."""
         old = self.table
+        on_gpu = self.device.type == "cuda"
+        if on_gpu:
+            torch.cuda.synchronize(self.device)
         new_slots = old.shape[0] * 2
-        self.table = torch.zeros(new_slots, self.stride, dtype=torch.int32, device=self.device)
-        self.table[: old.shape[0]].copy_(old)
+        table = torch.zeros(new_slots, self.stride, dtype=torch.int32, device=self.device)
+        table[: old.shape[0]].copy_(old)
+        if on_gpu:
+            torch.cuda.synchronize(self.device)
+        self.table = table
         self._free_slots = list(range(new_slots - 1, old.shape[0] - 1, -1)) + self._free_slots
 
     def acquire(self, state: KVRequestState) -> int:
@@ -182,6 +208,25 @@ class DeviceBlockTable:
                 state._dev_list = None
                 state._dev_len = 0
 
+    @staticmethod
+    def _synced_prefix(st: KVRequestState, pl: list, n: int) -> int:
+        """Leading pages of ``pl`` that the device row already holds: the
+        synced length when ``pl`` is the synced list object, at least as long
+        as then, with its first page and its last synced page unchanged;
+        otherwise 0 (the whole list is sent)."""
+        m = st._dev_len
+        if st._dev_list is not pl or n < m:
+            return 0
+        if m and (pl[0], pl[m - 1]) != st._dev_ends:
+            return 0
+        return m
+
+    @staticmethod
+    def _mark_synced(st: KVRequestState, pl: list, n: int) -> None:
+        st._dev_list = pl
+        st._dev_len = n
+        st._dev_ends = (pl[0], pl[n - 1]) if n else (-1, -1)
+
     def prepare(self, states: list[KVRequestState]) -> tuple[np.ndarray, np.ndarray]:
         """What ``mi_pack`` must add to the table for ``states``: per state the
         number of leading pages already on the device, and all the other pages
@@ -195,12 +240,11 @@ class DeviceBlockTable:
             n = len(pl)
             if n > self.stride:
                 raise ValueError(f"request holds {n} pages, block table rows hold {self.stride}")
-            start = st._dev_len if (st._dev_list is pl and n >= st._dev_len) else 0
+            start = self._synced_prefix(st, pl, n)
             old[i] = start
             if n > start:
                 parts.append(pl[start:])
-            st._dev_list = pl
-            st._dev_len = n
+            self._mark_synced(st, pl, n)
         new = np.fromiter((p for part in parts for p in part), dtype=np.int32) if parts else np.zeros(0, np.int32)
         return old, new
 
@@ -214,16 +258,15 @@ class DeviceBlockTable:
                 self.acquire(st)
             pl = st.page_indices
             n = len(pl)
-            if st._dev_list is pl and n == st._dev_len:  # nothing new (most requests of a decode step)
-                start = n
+            if st._dev_list is pl and n == st._dev_len and (not n or (pl[0], pl[n - 1]) == st._dev_ends):
+                start = n  # nothing new (most requests of a decode step)
             else:
                 if n > stride:
                     raise ValueError(f"request holds {n} pages, block table rows hold {stride}")
-                start = st._dev_len if (st._dev_list is pl and n >= st._dev_len) else 0
+                start = self._synced_prefix(st, pl, n)
                 if n > start:
                     parts.append(pl[start:])
-                st._dev_list = pl
-                st._dev_len = n
+                self._mark_synced(st, pl, n)
             slots.append(st.slot)
             npg.append(n)
             old.append(start)
@@ -240,13 +283,12 @@ class DeviceBlockTable:
             n = len(pl)
             if n > self.stride:
                 raise ValueError(f"request holds {n} pages, block table rows hold {self.stride}")
-            start = st._dev_len if (st._dev_list is pl and n >= st._dev_len) else 0
+            start = self._synced_prefix(st, pl, n)
             if n > start:
                 slots.append(np.full(n - start, slot, dtype=np.int32))
                 poss.append(np.arange(start, n, dtype=np.int32))
                 pages.append(np.asarray(pl[start:], dtype=np.int32))
-            st._dev_list = pl
-            st._dev_len = n
+            self._mark_synced(st, pl, n)
         if not slots:
             return
         upd = np.concatenate([np.concatenate(slots), np.concatenate(poss), np.concatenate(pages)])
@@ -347,10 +389,15 @@ class PagedAllocationManager:
                 state.page_indices.extend(new_pages)
 
     def alloc_batch(self, entries: list[tuple[str, str]], states: list[KVRequestState],
-                    seq_lens_after: np.ndarray) -> None:
+                    seq_lens_after: np.ndarray, generation: int | None = None) -> None:
         """``alloc(rid, label, seq_lens_after[i])`` for every entry, in order.
 
-        ``states[i]`` is the state of ``entries[i]``.  When the free list holds
+        ``states[i]`` is the caller's state object for ``entries[i]``, looked
+        up when ``state_generation`` read ``generation``.  If a state was
+        replaced or removed since (another thread's ``reset_label`` or
+        ``remove_request``), the live state is looked up under the lock, as
+        ``alloc`` does, and written back into ``states``, so pages never go to
+        a state that is no longer the request's.  When the free list holds
         every page the batch needs, the pages are taken in one pass and handed
         out in entry order, which is what the sequential calls would give;
         otherwise the entries are allocated one by one, so the first one that
@@ -359,6 +406,11 @@ class PagedAllocationManager:
         """
         ps = self.config.page_size
         with self._lock:
+            if generation is None or generation != self.state_generation:
+                for i, (rid, label) in enumerate(entries):
+                    live = self.get_state(rid, label)
+                    if live is not states[i]:
+                        states[i] = live
             npg = np.array([len(st.page_indices) for st in states], dtype=np.int64)
             need = (np.asarray(seq_lens_after, dtype=np.int64) + ps - 1) // ps - npg
             idx = np.flatnonzero(need > 0).tolist()
@@ -420,23 +472,34 @@ class PagedAllocationManager:
             self._kv_transfer_engine = DeviceKVTransferEngine(self.kv_cache)
         return self._kv_transfer_engine
 
+    def _settle_reads(self, request_id: str, label: str, block: bool) -> bool:
+        """Forget the finished reads of (request, label); with ``block``, wait
+        for all of them first.  Keeps the state's ``read_in_progress`` equal to
+        "a read is still outstanding" and returns True when none is."""
+        per_label = self.pending_reads.get(request_id)
+        futures = per_label.get(label, []) if per_label is not None else []
+        if block:
+            for f in futures:
+                f.result()
+            left = []
+        else:
+            left = [f for f in futures if not f.done()]
+        if per_label is not None:
+            per_label[label] = left
+        state = self.request_states.get(request_id, {}).get(label)
+        if state is not None:
+            state.read_in_progress = bool(left)
+        return not left
+
     def wait_for_retrieves(self, request_id: str, label: str) -> None:
-        for future in self.pending_reads.get(request_id, {}).get(label, []):
-            future.result()
-        if label in self.request_states.get(request_id, {}):
-            self.request_states[request_id][label].read_in_progress = False
-        if request_id in self.pending_reads:
-            self.pending_reads[request_id][label] = []
+        """Block until every read into (request, label) has landed (``kv_store.py:484-491``)."""
+        self._settle_reads(request_id, label, block=True)
 
     def check_retrieve_ready(self, request_id: str, label: str) -> bool:
         """True once every read of (request, label) has finished (``kv_store.py:493-509``)."""
-        state = self.get_state(request_id, label)
-        if not state.read_in_progress:
+        if not self.get_state(request_id, label).read_in_progress:
             return True
-        futures = [f for f in self.pending_reads[request_id].get(label, []) if not f.done()]
-        state.read_in_progress = len(futures) > 0
-        self.pending_reads[request_id][label] = futures
-        return not state.read_in_progress
+        return self._settle_reads(request_id, label, block=False)
 
     def sync_retrieve(self, request_id: str, label: str, seq_info) -> None:
         self.start_async_retrieve(request_id, label, seq_info)
@@ -490,36 +553,54 @@ class PagedAllocationManager:
     # ----- CPU offloading (kv_store.py:617-660) -----
 
     def offload_request(self, request_id: str, cpu_pool) -> int:
-        """Offload every label of a request to ``cpu_pool`` and free its GPU pages.
+        """Move every label of a request that holds pages to ``cpu_pool`` and
+        give its GPU pages back (``kv_store.py:617-644``); returns the number
+        of GPU pages freed.
 
-        As in the reference, a label whose CPU pages run out is not recorded
-        by the pool but its GPU pages are still freed.
+        Per label: reads into it land first, its copy is queued (the pool makes
+        the caller's stream wait for the copy, so the freed pages cannot be
+        overwritten before they are read), then its pages return to the FIFO
+        tail in list order and the state empties.  A label the CPU pool has no
+        room for is not recorded there, and its GPU pages are freed anyway, as
+        in the reference.  The manager lock is held only for the bookkeeping,
+        never while waiting on reads or queueing copies, so a plan thread can
+        keep allocating meanwhile.
         """
-        freed = 0
         with self._lock:
-            labels = list(self.request_states[request_id].items())
-        for label, state in labels:
-            if not state.page_indices:
-                continue
+            holding = [(label, st) for label, st in self.request_states[request_id].items() if st.page_indices]
+        freed = 0
+        for label, st in holding:
             self.wait_for_retrieves(request_id, label)
-            cpu_pool.offload_pages(request_id, label, self.kv_cache, state.page_indices, state.seq_len,
-                                   state.position_id_start)
+            cpu_pool.offload_pages(request_id, label, self.kv_cache, st.page_indices, st.seq_len,
+                                   st.position_id_start)
             with self._lock:
-                freed += len(state.page_indices)
-                self.page_allocator.free(state.page_indices)
-                state.page_indices = []
-                state.seq_len = 0
+                pages, st.page_indices, st.seq_len = st.page_indices, [], 0
+                self.page_allocator.free(pages)
+            freed += len(pages)
         return freed
 
     def reload_request(self, request_id: str, cpu_pool) -> None:
-        """Reload every offloaded label of a request into fresh GPU pages (``RuntimeError`` when short)."""
+        """Bring every offloaded label of a request back into fresh GPU pages
+        (``kv_store.py:646-660``).
+
+        The pages of all labels are taken from the free list in one call and
+        dealt out in label order, which gives each label the page ids the
+        reference's label-by-label allocation gives.  A pool too small for the
+        whole request raises ``RuntimeError`` before any label changes (the
+        reference raises at the first label that does not fit, after
+        reloading the ones before it).  One copy per label goes to the pool's
+        stream; the caller's stream waits for all of them at the end.
+        """
         with self._lock:
-            for label in list(cpu_pool.offloaded.get(request_id, {}).keys()):
-                n = len(cpu_pool.offloaded[request_id][label].cpu_page_indices)
-                pages = self.page_allocator.allocate(n)
-                state = self.get_state(request_id, label)
-                state.page_indices = pages
-                seq_len, pos = cpu_pool.reload_pages(request_id, label, self.kv_cache, pages)
-                state.seq_len = seq_len
-                state.position_id_start = pos
+            held = cpu_pool.offloaded.get(request_id, {})
+            labels = list(held)
+            counts = [len(held[label].cpu_page_indices) for label in labels]
+            pages = self.page_allocator.allocate(sum(counts))
+            start = 0
+            for label, n in zip(labels, counts):
+                mine = pages[start:start + n]
+                start += n
+                st = self.get_state(request_id, label)
+                seq_len, pos = cpu_pool.reload_pages(request_id, label, self.kv_cache, mine)
+                st.page_indices, st.seq_len, st.position_id_start = mine, seq_len, pos
         cpu_pool.sync()

@@ -378,7 +378,9 @@ class PagedPrefillWrapper(_FusedRopeAppend):
         self.causal = True
         self._workspace = workspace_buffer
         self._staging = _Staging()
-        self._side: torch.cuda.Stream | None = None
+        # Side stream of run(): made here so that a run() under graph capture
+        # only records the fork/join on it (creating a stream is not capturable).
+        self._side = torch.cuda.Stream(device=self.device)
         self._n_req = 0
         if use_cuda_graph:
             assert batch_size is not None, "batch_size required for CUDA graph mode"
@@ -499,8 +501,6 @@ class PagedPrefillWrapper(_FusedRopeAppend):
         # short-query requests write disjoint rows: run the HBM-bound decode
         # on a side stream so it overlaps the compute-bound tiles.
         main = torch.cuda.current_stream(q.device)
-        if self._side is None:
-            self._side = torch.cuda.Stream(device=q.device)
         side = self._side
         side.wait_stream(main)
         args[-1] = main.cuda_stream

@@ -175,7 +175,16 @@ def test_cpu_offload_reload_round_trip(gpu):
     mgr.add_request("z", ["main"])
     mgr.alloc("z", "main", 81 * ps)
     kv[:, mgr.get_state("z", "main").page_indices] = 0
+    mgr.add_request("y", ["main"])
+    mgr.alloc("y", "main", 1)  # 14 GPU pages left: c (9) fits, then a (5 + 1) does not
     mgr.reload_request("c", cpu_pool)
+    free_before = list(mgr.page_allocator.free_pages)
+    with pytest.raises(RuntimeError):
+        mgr.reload_request("a", cpu_pool)  # all-or-nothing: no label of "a" changes
+    assert list(mgr.page_allocator.free_pages) == free_before
+    assert cpu_pool.is_offloaded("a") and set(cpu_pool.offloaded["a"]) == {"main", "cfg"}
+    assert mgr.get_state("a", "main").page_indices == [] and mgr.get_state("a", "cfg").page_indices == []
+    mgr.remove_request("y")
     mgr.reload_request("a", cpu_pool)
     torch.cuda.synchronize()
     assert mgr.num_free_pages == 0
