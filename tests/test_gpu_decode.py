@@ -21,7 +21,7 @@ TOL_FP8 = 6e-2
 
 
 def _run_decode(gpu, hq, hkv, d, ps, kv_indptr, kv_indices, last, pool, seed, dtype=torch.bfloat16,
-                fp8=False, cpu_index=True):
+                fp8=False, cpu_index=True, ws_bytes=256 << 20, plan_header=None):
     b = len(last)
     g = torch.Generator().manual_seed(seed + 1000)
     cache_src = random_cache(pool, ps, hkv, d, seed, torch.float32)
@@ -45,7 +45,7 @@ def _run_decode(gpu, hq, hkv, d, ps, kv_indptr, kv_indices, last, pool, seed, dt
     A.append(cache_cpu, loc[:, 0], loc[:, 1], k_new, v_new, ks, vs)
     ref = decode_reference(q, cache_cpu, kv_indptr, kv_indices, last, ks, vs)
 
-    wrapper = FlashInferDecodeWrapper(workspace(gpu), hq, hkv, d, ps, device=gpu)
+    wrapper = FlashInferDecodeWrapper(workspace(gpu, ws_bytes), hq, hkv, d, ps, device=gpu)
     t = (lambda x: torch.as_tensor(x)) if cpu_index else (lambda x: torch.as_tensor(x).to(gpu))
     wrapper.plan(t(kv_indptr), t(kv_indices), t(last), dtype=dtype)
     wrapper.set_kv_cache(cache, k_new.to(gpu), v_new.to(gpu), *scales)
@@ -53,6 +53,8 @@ def _run_decode(gpu, hq, hkv, d, ps, kv_indptr, kv_indices, last, pool, seed, dt
     torch.cuda.synchronize()
     assert torch.equal(cache.cpu().view(torch.uint8), cache_cpu.view(torch.uint8)), "append is not bit-exact"
     assert torch.equal(wrapper.kv_cache_locations.cpu(), torch.as_tensor(loc)), "write locations differ"
+    if plan_header is not None:  # [magic, batch, items, item_pages, max_items] of the split-KV plan
+        plan_header.extend(wrapper._workspace[:20].view(torch.int32).cpu().tolist())
     return out, ref
 
 
@@ -133,3 +135,35 @@ def test_decode_is_deterministic(gpu):
     b = w.run(q, cache)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def _ws_for_items(batch, hkv, d, items):
+    """Workspace bytes whose split-KV plan holds at most ``items`` items: the
+    plan header, item offsets and, per item, its work entry and fp32 partial
+    (o, lse) of 16 rows per kv-head, plus alignment slack."""
+    fixed = 256 + -(-4 * (batch + 1) // 256) * 256 + 3 * 256
+    per_item = 16 + 4 * hkv * 16 + 4 * hkv * 16 * d
+    return fixed + per_item * items
+
+
+@pytest.mark.parametrize(
+    "hq,hkv,d,ps,fp8",
+    [(32, 4, 128, 16, False), (32, 4, 128, 32, False), (32, 4, 128, 16, True), (32, 4, 128, 32, True),
+     (8, 1, 256, 16, False), (24, 8, 64, 64, False)],
+)
+def test_decode_long_items_walk_several_page_windows(gpu, hq, hkv, d, ps, fp8):
+    """A workspace with room for batch + 2 items makes the plan cut long items
+    (over 256 pages, more than 64 pages per wavefront): each wavefront reloads
+    its window of page ids several times, at page sizes where a wavefront's
+    first token falls mid-page, and the longest request is still split in two
+    (partials + merge)."""
+    lens = [40000, 3000, 17]
+    qo, kv_indptr, kv_indices, last = custom_batch(lens, ps, 3000, seed=ps + d)
+    hdr = []
+    out, ref = _run_decode(gpu, hq, hkv, d, ps, kv_indptr, kv_indices, last, 3000, seed=ps + d + 1, fp8=fp8,
+                           ws_bytes=_ws_for_items(len(lens), hkv, d, len(lens) + 2), plan_header=hdr)
+    err = max_abs(out, ref)
+    log(f"decode long items hq={hq} hkv={hkv} d={d} ps={ps} fp8={fp8}: items={hdr[2]} item_pages={hdr[3]} "
+        f"max_abs={err:.3e}")
+    assert hdr[3] > 256 and hdr[2] == len(lens) + 1
+    assert err < (TOL_FP8 if fp8 else TOL_BF16)
