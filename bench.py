@@ -47,16 +47,19 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 METRIC = "paged decode attn tokens/s + achieved HBM GB/s (% peak), 1 MI355X, B=256"
 
 
-def measured_traffic(config: str) -> int | None:
-    """``traffic_bytes_per_launch`` from the committed rocprofv3 --pmc summary, or None."""
+def measured_traffic(config: str) -> tuple[int | None, int | None]:
+    """(``traffic_bytes_per_launch``, ``algorithmic_bytes_per_launch``) from the
+    committed rocprofv3 --pmc summary of ``config``, or (None, None)."""
+    vals = {}
     try:
         with open(TRAFFIC_PROFILE.format(config=config)) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1].strip())
+                for key in ("traffic_bytes_per_launch", "algorithmic_bytes_per_launch"):
+                    if line.startswith(key + ":"):
+                        vals[key] = int(line.split(":", 1)[1].strip())
     except OSError:
         pass
-    return None
+    return vals.get("traffic_bytes_per_launch"), vals.get("algorithmic_bytes_per_launch")
 
 
 def _log(msg: str) -> None:
@@ -64,44 +67,66 @@ def _log(msg: str) -> None:
 
 
 def fill_pool(kv: torch.Tensor, spec, device: torch.device):
-    """N(0,1) K/V drawn in bf16 from a seeded device generator.
+    """N(0,1) K/V drawn in bf16 from a seeded device generator, every layer.
 
-    An fp8 pool is quantised per (K|V, kv-head) with s = amax/448 over the
-    whole pool (two passes over the same draws); returns the fp32 scales
-    ``[1, 2, num_kv_heads]`` or None for a bf16 pool.
+    An fp8 pool is quantised per (layer, K|V, kv-head) with s = amax/448 over
+    the layer (two passes over the same draws); returns the fp32 scales
+    ``[layers, 2, num_kv_heads]`` or None for a bf16 pool.
     """
     gen = torch.Generator(device=device).manual_seed(spec.seed)
     chunk = 1 << 14
     pages = kv.shape[1]
     if kv.dtype != torch.float8_e4m3fn:
-        for p0 in range(0, pages, chunk):
-            kv[0, p0:p0 + chunk].normal_(generator=gen)
+        for layer in range(kv.shape[0]):
+            for p0 in range(0, pages, chunk):
+                kv[layer, p0:p0 + chunk].normal_(generator=gen)
         return None
     tmp = torch.empty((chunk,) + tuple(kv.shape[2:]), dtype=torch.bfloat16, device=device)
-    amax = torch.zeros(2, spec.num_kv_heads, device=device)
-    state = gen.get_state()
-    for p0 in range(0, pages, chunk):
-        t = tmp[:min(chunk, pages - p0)].normal_(generator=gen)
-        amax = torch.maximum(amax, t.abs().amax(dim=(0, 2, 4)).float())
-    scales = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
-    inv = (1.0 / scales).view(1, 2, 1, spec.num_kv_heads, 1)
-    gen.set_state(state)
-    for p0 in range(0, pages, chunk):
-        n = min(chunk, pages - p0)
-        t = tmp[:n].normal_(generator=gen)
-        kv[0, p0:p0 + n] = (t.float() * inv).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
-    return scales.view(1, 2, spec.num_kv_heads).contiguous()
+    all_scales = []
+    for layer in range(kv.shape[0]):
+        amax = torch.zeros(2, spec.num_kv_heads, device=device)
+        state = gen.get_state()
+        for p0 in range(0, pages, chunk):
+            t = tmp[:min(chunk, pages - p0)].normal_(generator=gen)
+            amax = torch.maximum(amax, t.abs().amax(dim=(0, 2, 4)).float())
+        scales = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+        inv = (1.0 / scales).view(1, 2, 1, spec.num_kv_heads, 1)
+        gen.set_state(state)
+        for p0 in range(0, pages, chunk):
+            n = min(chunk, pages - p0)
+            t = tmp[:n].normal_(generator=gen)
+            kv[layer, p0:p0 + n] = (t.float() * inv).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        all_scales.append(scales)
+    return torch.stack(all_scales).contiguous()
 
 
-def setup(spec_name: str, device: torch.device):
+# Layers of the pool a decode bench cycles through: one per step, as a
+# model's layer-steps would.  A working set below the 256 MB MALL (c1, and
+# c2 at 323 MB) would otherwise be served partly from the MALL when the same
+# layer is read step after step; three layers put about 1 GB between two
+# reads of the same pages.
+MALL_BYTES = 256 << 20
+
+
+def decode_layers(bt) -> int:
+    s = bt.spec
+    elem = 1 if s.kv_dtype == "fp8" else 2
+    working = bt.total_kv_tokens * s.num_kv_heads * s.head_dim * 2 * elem
+    return 3 if working < 4 * MALL_BYTES else 1
+
+
+def setup(spec_name: str, device: torch.device, layers: int | None = None):
     bt = S.make_batch(spec_name)
     s = bt.spec
     b = len(bt.kv_len)
-    cfg = KVCacheConfig(num_layers=1, num_kv_heads=s.num_kv_heads, head_dim=s.head_dim,
+    if layers is None:
+        layers = decode_layers(bt)
+    cfg = KVCacheConfig(num_layers=layers, num_kv_heads=s.num_kv_heads, head_dim=s.head_dim,
                         max_seq_len=40960, max_num_pages=s.pool_pages, page_size=s.page_size,
                         num_qo_heads=s.num_qo_heads)
     kv_dtype = torch.float8_e4m3fn if s.kv_dtype == "fp8" else torch.bfloat16
-    kv = torch.empty(1, s.pool_pages, 2, s.page_size, s.num_kv_heads, s.head_dim, dtype=kv_dtype, device=device)
+    kv = torch.empty(layers, s.pool_pages, 2, s.page_size, s.num_kv_heads, s.head_dim, dtype=kv_dtype,
+                     device=device)
     scales = fill_pool(kv, s, device)
     mgr = PagedAllocationManager(cfg, kv, device=device)
     # Steady state: each request already holds its T-1 cached tokens on the
@@ -139,34 +164,39 @@ def decode_bytes(seq_lens_after: np.ndarray, total_pages: int, s) -> int:
     return kv + qo + idx + scales
 
 
-def _layer_scales(cm):
+def _layer_scales(cm, layer: int = 0):
     if cm.kv_scales is None:
         return None, None
-    return cm.kv_scales[0, 0], cm.kv_scales[0, 1]
+    return cm.kv_scales[layer, 0], cm.kv_scales[layer, 1]
 
 
-def step_once(cm, q, k, v, b, events=None):
+def step_once(cm, q, k, v, b, events=None, layer: int = 0):
+    """One layer-step: plan (pack + split-KV plan), append, decode + merge, advance."""
     cm.plan_attention([1] * b)
     wrapper = cm._plan_states["main"].wrapper
-    layer = cm.kv_cache[0]
-    ks, vs = _layer_scales(cm)
-    wrapper.set_kv_cache(layer, k, v, k_scale=ks, v_scale=vs)
+    kv_layer = cm.kv_cache[layer]
+    ks, vs = _layer_scales(cm, layer)
+    wrapper.set_kv_cache(kv_layer, k, v, k_scale=ks, v_scale=vs)
     if events is None:
-        out = wrapper.run(q, layer, k_scale=ks, v_scale=vs)
+        out = wrapper.run(q, kv_layer, k_scale=ks, v_scale=vs)
     else:
-        out = _run_split(wrapper, q, layer, ks, vs, events)
+        out = _run_split(wrapper, q, kv_layer, ks, vs, events)
     cm.advance_seq_lens()
     return out
 
 
-def _run_split(w, q, layer, ks, vs, events):
-    """wrapper.run() as its two C entry points, with HIP events around the decode kernel."""
-    desc = _lib.paged_kv_desc(layer, ks, vs)
-    out = torch.empty_like(q)
-    args = (q.data_ptr(), _lib.MI_BF16, q.stride(0), q.stride(1), desc, None, w._indptr.data_ptr(),
+def _decode_args(w, q, kv_layer, ks, vs, out):
+    desc = _lib.paged_kv_desc(kv_layer, ks, vs)
+    return (q.data_ptr(), _lib.MI_BF16, q.stride(0), q.stride(1), desc, None, w._indptr.data_ptr(),
             w._indices.data_ptr(), w._last.data_ptr(), w._n_req, w.num_qo_heads, 0, 1.0 / math.sqrt(w.head_dim),
             w._workspace.data_ptr(), w._workspace.numel(), out.data_ptr(), out.stride(0), out.stride(1),
             _lib.stream_ptr(q.device))
+
+
+def _run_split(w, q, kv_layer, ks, vs, events):
+    """wrapper.run() as its two C entry points, with HIP events around the decode kernel."""
+    out = torch.empty_like(q)
+    args = _decode_args(w, q, kv_layer, ks, vs, out)
     e0, e1, e2 = events
     e0.record()
     _lib.check(_lib.lib().mi_decode_attend(*args), "mi_decode_attend")
@@ -176,33 +206,83 @@ def _run_split(w, q, layer, ks, vs, events):
     return out
 
 
-def cpu_baseline(bt, kv_gpu, q, k, v, scales=None, budget_s: float = 12.0):
-    """The CPU restatement (oracle/) on a sample of the batch: pack + append + fp32 attention."""
+def decode_graph_us(cm, q, steps: int, per_layer: int = 4) -> tuple[float, float]:
+    """(decode kernel us, decode + merge us) per launch of the current plan, from
+    HIP graph replays: ``per_layer`` launches on every layer of the pool, in
+    turn, captured into one graph; HIP events around each replay on the
+    launch stream.  Replays time the GPU alone, without the host issue gaps
+    that sit between a short kernel and the events around it."""
+    w = cm._plan_states["main"].wrapper
+    layers = cm.kv_cache.shape[0]
+    out = torch.empty_like(q)
+    argv = [_decode_args(w, q, cm.kv_cache[i], *_layer_scales(cm, i), out) for i in range(layers)]
+    L = _lib.lib()
+    n = per_layer * layers
+
+    def attend():
+        for i in range(n):
+            _lib.check(L.mi_decode_attend(*argv[i % layers][:-1], _lib.stream_ptr(q.device)), "mi_decode_attend")
+
+    def both():
+        for i in range(n):
+            a = (*argv[i % layers][:-1], _lib.stream_ptr(q.device))
+            _lib.check(L.mi_decode_attend(*a), "mi_decode_attend")
+            _lib.check(L.mi_decode_merge(*a), "mi_decode_merge")
+
+    return (_graph_us(attend, q.device, steps, per_graph=1) / n, _graph_us(both, q.device, steps, per_graph=1) / n)
+
+
+def host_cpu() -> dict:
+    """The host's CPU as /proc/cpuinfo names it, and its logical CPU count."""
+    info = {"model": "", "family": "", "model_number": "", "stepping": "", "logical_cpus": os.cpu_count()}
+    keys = {"model name": "model", "cpu family": "family", "model": "model_number", "stepping": "stepping"}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if ":" not in line:
+                    if info["model"]:
+                        break  # first processor block read
+                    continue
+                k, v = (x.strip() for x in line.split(":", 1))
+                if k in keys and not info[keys[k]]:
+                    info[keys[k]] = v
+    except OSError:
+        pass
+    return info
+
+
+def cpu_baseline(bt, kv_gpu, q, k, v, scales=None, budget_s: float = 20.0, min_runs: int = 2):
+    """The CPU restatement (oracle/) of one whole step of the batch: FIFO pack, append,
+    fp32 paged attention, on the host threads this process is given.
+
+    Runs the whole batch until ``budget_s`` has passed and at least
+    ``min_runs`` runs are done; reports the median.  Layer 0 of the pool, the
+    batch's pages only (copied to host memory once, outside the timing)."""
     from oracle import attention as A
     from oracle import packing as P
 
     s = bt.spec
-    threads = min(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), 16)
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    nreq = 16
-    sub = S.truncate(bt, nreq)
-    pages = sub.kv_indices
+    nreq = len(bt.kv_len)
+    pages = bt.kv_indices
     uniq = np.unique(pages)
-    remap = {int(p): i for i, p in enumerate(uniq)}
+    remap = np.zeros(s.pool_pages, dtype=np.int64)
+    remap[uniq] = np.arange(len(uniq))
     cache = kv_gpu[0, torch.as_tensor(uniq, device=kv_gpu.device)].cpu()
-    idx = np.asarray([remap[int(p)] for p in pages], dtype=np.int32)
+    idx = remap[pages].astype(np.int32)
     qc, kc, vc = q[:nreq].cpu(), k[:nreq].cpu(), v[:nreq].cpu()
     ks = vs = None
     if scales is not None:
         ks, vs = scales[0, 0].cpu(), scales[0, 1].cpu()
     times = []
     t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
+    while len(times) < min_runs or time.perf_counter() < t_end:
         t0 = time.perf_counter()
         states, extra = [], []
         for i in range(nreq):
-            pl = idx[sub.kv_indptr[i]:sub.kv_indptr[i + 1]].tolist()
-            cached = int(sub.kv_len[i]) - 1
+            pl = idx[bt.kv_indptr[i]:bt.kv_indptr[i + 1]].tolist()
+            cached = int(bt.kv_len[i]) - 1
             keep = -(-cached // s.page_size)
             states.append(P.ReqState(pages=pl[:keep], seq_len=cached))
             extra += pl[keep:]  # a page the new token opens comes from the free list
@@ -214,26 +294,21 @@ def cpu_baseline(bt, kv_gpu, q, k, v, scales=None, budget_s: float = 12.0):
         A.paged_attention(qc, cache, None, packed.kv_indptr, packed.kv_indices, packed.last_page_len, causal=False,
                           k_scale=ks, v_scale=vs)
         times.append(time.perf_counter() - t0)
-        if len(times) >= 10 and time.perf_counter() > t_end:
-            break
     med = float(np.median(times))
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    cpu = host_cpu()
     return {
         "value": nreq / med,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"first {nreq} of the {len(bt.kv_len)} {s.name} requests ({int(sub.kv_len.sum())} KV tokens), "
-                   f"pack + append + fp32 paged attention, median of {len(times)} runs, "
-                   f"{threads} host threads, CPU: {model}"),
+        "ms_per_step": med * 1e3,
+        "host_logical_cpus": cpu["logical_cpus"],
+        "cpu_model": cpu["model"],
+        "cpu_family_model_stepping": f"{cpu['family']}/{cpu['model_number']}/{cpu['stepping']}",
+        "sample": (f"the whole {s.name} step: {nreq} requests, {int(bt.kv_len.sum())} KV tokens; FIFO pack + append "
+                   f"+ fp32 paged attention (oracle/), median of {len(times)} runs, {torch.get_num_threads()} host "
+                   f"threads (this process's share of the box's {cpu['logical_cpus']} logical CPUs), "
+                   f"CPU: {cpu['model']}"),
     }
 
 
@@ -256,6 +331,7 @@ def copy_calibration(dev) -> int:
 
 
 WORKLOADS = {
+    "c1": "c1: CPU-baseline decode shape (B=8, 8 q / 2 kv heads), one layer-step of pack+plan+append+decode+merge",
     "c2": "c2: Orpheus (Llama-3.2-3B) decode, one layer-step of pack+plan+append+decode+merge",
     "c3": "c3: Qwen3-Omni thinker decode, one layer-step of pack+plan+append+decode+merge",
     "c4": "c4: BAGEL (Qwen2.5-7B) ragged chunked prefill + decode mix, one layer-step of plan+append+attention",
@@ -272,18 +348,19 @@ def bench_decode(args, dev) -> dict:
     bt, cfg, kv, mgr, cm, rids, q, k, v = setup(args.config, dev)
     s = bt.spec
     b = len(rids)
+    layers = kv.shape[0]
     torch.cuda.synchronize()
     _log(f"warmup {args.warmup} steps")
-    for _ in range(args.warmup):
-        step_once(cm, q, k, v, b)
+    for i in range(args.warmup):
+        step_once(cm, q, k, v, b, layer=i % layers)
     torch.cuda.synchronize()
 
     # timed region 1: the full hot path per step, wall clock
     _log(f"timing {args.steps} steps")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step_once(cm, q, k, v, b)
+    for i in range(args.steps):
+        step_once(cm, q, k, v, b, layer=i % layers)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / args.steps
 
@@ -292,15 +369,20 @@ def bench_decode(args, dev) -> dict:
     bytes_per = []
     for i in range(args.steps):
         seq_after = np.array([cm._get_state(r).seq_len + 1 for r in rids])
-        step_once(cm, q, k, v, b, events=evs[i])
+        step_once(cm, q, k, v, b, events=evs[i], layer=i % layers)
         bytes_per.append(decode_bytes(seq_after, sum(len(cm._get_state(r).page_indices) for r in rids), s))
     torch.cuda.synchronize()
     dec_ms = np.array([e0.elapsed_time(e1) for e0, e1, _ in evs])
     dm_ms = np.array([e0.elapsed_time(e2) for e0, _, e2 in evs])
-    dec_s = float(dec_ms.mean()) / 1e3
-    achieved = float(np.mean(bytes_per)) / dec_s / 1e9
-    kv_tokens = int(sum(cm._get_state(r).seq_len for r in rids))
+
+    # timed region 3: the last step's plan, decode (and merge) launches replayed from a HIP graph
+    seq_now = np.array([cm._get_state(r).seq_len for r in rids])
+    graph_bytes = decode_bytes(seq_now, sum(len(cm._get_state(r).page_indices) for r in rids), s)
+    dec_us, dm_us = decode_graph_us(cm, q, args.steps)
+    achieved = graph_bytes / (dec_us * 1e-6) / 1e9
+    kv_tokens = int(seq_now.sum())
     lo, hi = s.ctx[1], s.ctx[2]
+    traffic, traffic_alg = measured_traffic(s.name)
     res = {
         "metric": METRIC if s.name == "c3" else f"paged decode attn tokens/s + achieved HBM GB/s, 1 MI355X, B={b}",
         "value": b / wall,
@@ -318,7 +400,7 @@ def bench_decode(args, dev) -> dict:
             "workload": WORKLOADS[s.name],
             "batch": b, "num_qo_heads": s.num_qo_heads, "num_kv_heads": s.num_kv_heads, "head_dim": s.head_dim,
             "page_size": s.page_size, "context": f"{s.ctx[0]} [{lo}, {hi}]", "kv_pool_pages": s.pool_pages,
-            "kv_dtype": s.kv_dtype, "kv_tokens_at_end": kv_tokens,
+            "kv_layers_cycled": layers, "kv_dtype": s.kv_dtype, "kv_tokens_at_end": kv_tokens,
         },
         "roofline": {
             "bound": "hbm",
@@ -326,22 +408,29 @@ def bench_decode(args, dev) -> dict:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": measured_traffic(s.name),
+            "traffic": traffic,
+            "traffic_source": (f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes over the {s.name} bench, scaled by a "
+                               f"1 GiB copy; per decode launch of a plan with {traffic_alg} algorithmic bytes"
+                               if traffic is not None else None),
             "kernel": "decode_kernel",
-            "kernel_us": dec_s * 1e6,
-            "kernel_us_median": float(np.median(dec_ms)) * 1e3,
-            "decode_plus_merge_us": float(dm_ms.mean()) * 1e3,
-            "algorithmic_bytes": int(np.mean(bytes_per)),
+            "kernel_us": dec_us,
+            "kernel_us_how": (f"HIP graph replay of {4 * layers} decode launches of the last step's plan "
+                              f"({layers} pool layer(s) in turn), HIP events on the launch stream"),
+            "algorithmic_bytes": graph_bytes,
+            "decode_plus_merge_us": dm_us,
+            "kernel_us_events_in_step_loop": float(dec_ms.mean()) * 1e3,
+            "decode_plus_merge_us_events_in_step_loop": float(dm_ms.mean()) * 1e3,
+            "algorithmic_bytes_step_loop_mean": int(np.mean(bytes_per)),
         },
     }
-    pos_now = np.array([cm._get_state(r).seq_len for r in rids])
+    pos_now = seq_now
     if not args.no_extra:
         res["rope"] = bench_rope(q, k, pos_now, args.steps)
         res["rope_append"] = bench_rope_append(cm, q, k, v, pos_now, args.steps)
         res["kv_transfer"] = bench_transfer(kv, args.steps)
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
-        res["cpu_baseline"] = cpu_baseline(bt, kv, q, k, v, cm.kv_scales)
+        res["cpu_baseline"] = cpu_baseline(bt, kv, q, k, v, cm.kv_scales, min_runs=10 if s.name == "c1" else 2)
     return res
 
 

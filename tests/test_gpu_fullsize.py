@@ -2,7 +2,7 @@
 
 c2 (B=64), c3 and c5 (B=256) are set up by ``bench.setup`` (the full KV pool,
 random pages, the steady-state FIFO free list) and stepped with
-``bench.step_once``: ``BatchedCacheManager.plan_attention([1]*B)`` (host FIFO
+``bench.step_once`` (on the pool layers the bench cycles through): ``BatchedCacheManager.plan_attention([1]*B)`` (host FIFO
 allocation, block-table delta, ``mi_pack_plan``), ``set_kv_cache``, ``run``
 (decode + merge), ``advance_seq_lens``.  Three steps each; per step:
 
@@ -64,16 +64,17 @@ def test_bench_step_parity(gpu, config):
     bt, cfg, kv, mgr, cm, rids, q, k, v = bench.setup(config, gpu)
     s = bt.spec
     b = len(rids)
-    layer = kv[0]
-    ks, vs = bench._layer_scales(cm)
     fp8 = s.kv_dtype == "fp8"
     for step in range(3):
+        li = step % kv.shape[0]  # the bench cycles the pool's layers when one layer's pages fit the MALL
+        layer = kv[li]
+        ks, vs = bench._layer_scales(cm, li)
         states = [mgr.get_state(r, "main") for r in rids]
         ostates = [P.ReqState(pages=list(st.page_indices), seq_len=st.seq_len) for st in states]
         pool = P.FifoPages(0)
         pool.free.extend(mgr.page_allocator.free_pages)
         want = P.pack(ostates, [1] * b, pool, s.page_size)
-        out = bench.step_once(cm, q, k, v, b)
+        out = bench.step_once(cm, q, k, v, b, layer=li)
         qo, ip, idx, last, loc = cm._last_pack
         torch.cuda.synchronize()
         got = [t.cpu().numpy() for t in (qo, ip, idx, last, loc)]
