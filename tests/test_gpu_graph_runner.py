@@ -10,7 +10,16 @@ stream (``plan_attention`` into the slot's wrapper, ``_pre_planned_labels``
 + a plan-done event), pads the real batch with dummy requests, replays, and
 checks every real request against a list-history oracle (RoPE'd K/V appended
 per step, fp32 attention over the whole history, max-abs <= 2e-2).
+
+With ``plan_thread`` the pre-plan runs as in M*'s worker
+(``cuda_graph_runner.py:1031-1078``, ``:1375-1396``): on a plan thread
+(one-worker executor) that starts once the replaying step has advanced its
+request states, while the engine thread frees the replayed slot's padding
+states and checks the outputs; the allocator, the device block table and the
+shared pinned uploader are then used from two threads at once.
 """
+
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -48,7 +57,8 @@ def _forward(s):
     return torch.stack(outs)
 
 
-def test_double_buffered_decode_graphs(gpu):
+@pytest.mark.parametrize("plan_thread", [False, True])
+def test_double_buffered_decode_graphs(gpu, plan_thread):
     cfg = KVCacheConfig(num_layers=LAYERS, num_kv_heads=HKV, head_dim=D, max_seq_len=4096, max_num_pages=POOL,
                         page_size=PS, num_qo_heads=HQ)
     kv = torch.zeros(LAYERS, POOL, 2, PS, HKV, D, dtype=torch.bfloat16, device=gpu)
@@ -130,9 +140,14 @@ def test_double_buffered_decode_graphs(gpu):
     schedule = [8, 8, 8, 6, 6, 5, 5, 8]  # real batch per step; finished requests leave, padding fills
     ev = pre_plan(0, live)
     main = torch.cuda.current_stream(gpu)
+    executor = ThreadPoolExecutor(max_workers=1) if plan_thread else None
+    fut = None
     for step, nreal in enumerate(schedule):
         s = step % 2
         sl = slots[s]
+        if fut is not None:
+            ev = fut.result()  # this slot's pre-plan, run on the plan thread
+            fut = None
         live_now = list(sl["cm"].request_ids[:len(live)])
         starts = [mgr.get_state(r, "main").position_id_start for r in live_now]
         # inputs for this step (real rows; padded rows get zeros)
@@ -150,8 +165,9 @@ def test_double_buffered_decode_graphs(gpu):
         # host bookkeeping of the step while the replay runs: advance, free padding,
         # batch changes, then pre-plan the other slot on the plan stream
         sl["cm"].advance_seq_lens()
-        for r in dummies[s][len(live_now):]:
-            mgr.reset_label(r, "main", free=True)
+        if not plan_thread:
+            for r in dummies[s][len(live_now):]:
+                mgr.reset_label(r, "main", free=True)
         if step + 1 < len(schedule):
             nxt = schedule[step + 1]
             while len(live) > nxt:  # a request finishes: its pages go back to the pool
@@ -161,7 +177,13 @@ def test_double_buffered_decode_graphs(gpu):
                 mgr.add_request(r, ["main"])
                 hist.update({(r, l): ([], []) for l in range(LAYERS)})
                 live.append(r)
-            ev = pre_plan((step + 1) % 2, live)
+            if plan_thread:
+                fut = executor.submit(pre_plan, (step + 1) % 2, list(live))
+            else:
+                ev = pre_plan((step + 1) % 2, live)
+        if plan_thread:  # engine-thread bookkeeping while the plan thread allocates
+            for r in dummies[s][len(live_now):]:
+                mgr.reset_label(r, "main", free=True)
         torch.cuda.synchronize()
         out = sl["out"].clone()
         worst = 0.0
@@ -176,3 +198,5 @@ def test_double_buffered_decode_graphs(gpu):
                 worst = max(worst, max_abs(out[layer, i:i + 1], o))
         log(f"step {step} slot {s}: real={len(live_now)} max_abs={worst:.3e}")
         assert worst < 2e-2
+    if executor is not None:
+        executor.shutdown()
