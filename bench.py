@@ -115,7 +115,7 @@ def decode_layers(bt) -> int:
     return 3 if working < 4 * MALL_BYTES else 1
 
 
-def setup(spec_name: str, device: torch.device, layers: int | None = None):
+def setup(spec_name: str, device: torch.device, layers: int | None = None, trace_ranges: bool = False):
     bt = S.make_batch(spec_name)
     s = bt.spec
     b = len(bt.kv_len)
@@ -145,7 +145,8 @@ def setup(spec_name: str, device: torch.device, layers: int | None = None):
         st.seq_len = int(bt.kv_len[i]) - 1
         st.position_id_start = st.seq_len
     bufs = WorkspaceBufferManager(512 << 20, device)  # the reference's per-label workspace size
-    cm = BatchedCacheManager(rids, {r: "main" for r in rids}, kv, mgr, bufs, cfg, device, kv_scales=scales)
+    cm = BatchedCacheManager(rids, {r: "main" for r in rids}, kv, mgr, bufs, cfg, device, kv_scales=scales,
+                             enable_nvtx=trace_ranges)
     g = torch.Generator().manual_seed(s.seed + 1)
     q = torch.randn(b, s.num_qo_heads, s.head_dim, generator=g).to(torch.bfloat16).to(device)
     k = torch.randn(b, s.num_kv_heads, s.head_dim, generator=g).to(torch.bfloat16).to(device)
@@ -345,7 +346,7 @@ def _kernel_events(n: int, k: int):
 
 def bench_decode(args, dev) -> dict:
     _log(f"setup {args.config} ...")
-    bt, cfg, kv, mgr, cm, rids, q, k, v = setup(args.config, dev)
+    bt, cfg, kv, mgr, cm, rids, q, k, v = setup(args.config, dev, trace_ranges=args.trace_ranges)
     s = bt.spec
     b = len(rids)
     layers = kv.shape[0]
@@ -780,6 +781,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true",
                     help="only the step loop: skip the side measurements (RoPE, KV transfer, "
                          "head_dim 256 and fp8-pool prefill), e.g. for counter runs")
+    ap.add_argument("--trace-ranges", action="store_true",
+                    help="decode configs: the manager pushes its tracing ranges (enable_nvtx), for rocprofv3 --marker-trace")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain device copy of 1 GiB (3x): the reference point that scales "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes")

@@ -32,6 +32,7 @@ from . import _lib
 from .kv_store import KVCacheConfig, KVRequestState, PagedAllocationManager
 from .paged_attention import PagedDecodeWrapper, PagedPrefillWrapper
 from .rope import apply_llama31_rope_pos_ids_inplace, apply_rope_pos_ids_inplace, rope_positions
+from .trace import trace_range
 
 _LLAMA31_KEYS = ("low_freq_factor", "high_freq_factor", "old_context_len")
 
@@ -147,15 +148,18 @@ class BatchedCacheManager:
     def plan_attention(self, seq_lens: list[int] | None = None, dtype: torch.dtype | None = None,
                        is_causal: bool = True, write_store: bool = True, label: str | None = None) -> None:
         """Allocate pages, pack the step on the GPU and plan the wrapper (``cache_manager.py:167-227``)."""
-        effective = label if label is not None else self._single_active_label()
-        if effective in self._pre_planned_labels:
-            self._pre_planned_labels.discard(effective)
-            ps = self._plan_states.get(effective)
-            if ps is not None:
-                ps.seq_lens = seq_lens
-                ps.write_store = write_store
-            return
-        self._plan_attention_impl(seq_lens, dtype, is_causal, write_store, effective)
+        nv = self.enable_nvtx
+        with trace_range(nv, "cache.plan_attention"):
+            effective = label if label is not None else self._single_active_label()
+            if effective in self._pre_planned_labels:
+                with trace_range(nv, "cache.plan_attention.skipped_pre_planned"):
+                    self._pre_planned_labels.discard(effective)
+                    ps = self._plan_states.get(effective)
+                    if ps is not None:
+                        ps.seq_lens = seq_lens
+                        ps.write_store = write_store
+                return
+            self._plan_attention_impl(seq_lens, dtype, is_causal, write_store, effective)
 
     def _alloc_entries(self, entries: list[tuple[str, str]], seq_lens, states=None,
                        generation: int | None = None) -> np.ndarray:
@@ -228,8 +232,11 @@ class BatchedCacheManager:
         cfg = self.kv_cache_config
         ps_ = cfg.page_size
         b = len(self.request_ids)
-        entries, states, gen = self._label_states(label)
-        meta = self._alloc_entries(entries, seq_lens, states, gen)
+        nv = self.enable_nvtx
+        # host side: FIFO allocation and the block-table delta (the reference builds its page lists here)
+        with trace_range(nv, "cache.plan_attention.build_lists"):
+            entries, states, gen = self._label_states(label)
+            meta = self._alloc_entries(entries, seq_lens, states, gen)
         total_pages = int(meta[3 * b:4 * b].sum())
         new_lens = meta[2 * b:3 * b]
         is_decode = bool((new_lens == 1).all())
@@ -268,15 +275,18 @@ class BatchedCacheManager:
         else:
             qo, kv_indptr, kv_indices, last, loc = _step_tensors(b, total_pages, is_decode, self.device)
         fused = isinstance(wrapper, PagedDecodeWrapper) and is_decode and (not graph_static or b == wrapper.batch_size)
-        self._launch_pack(meta, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=wrapper if fused else None)
+        # device side: one upload of the step's metadata and one pack launch (the reference's torch.tensor builds)
+        with trace_range(nv, "cache.plan_attention.make_tensors"):
+            self._launch_pack(meta, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=wrapper if fused else None)
         self._last_pack = (qo, kv_indptr, kv_indices[:total_pages], last, loc)
-        if fused:
-            wrapper._adopt_plan(kv_indptr, kv_indices[:total_pages], last, loc, dtype)
-        elif isinstance(wrapper, PagedDecodeWrapper):
-            wrapper.plan(kv_indptr, kv_indices[:total_pages], last, kv_cache_locations=loc, dtype=dtype)
-        else:
-            wrapper.plan_device(qo, kv_indptr, kv_indices[:total_pages], last, total_tokens=int(meta[2 * b:3 * b].sum()),
-                                causal=is_causal, dtype=dtype)
+        with trace_range(nv, "cache.plan_attention.wrapper_plan"):
+            if fused:
+                wrapper._adopt_plan(kv_indptr, kv_indices[:total_pages], last, loc, dtype)
+            elif isinstance(wrapper, PagedDecodeWrapper):
+                wrapper.plan(kv_indptr, kv_indices[:total_pages], last, kv_cache_locations=loc, dtype=dtype)
+            else:
+                wrapper.plan_device(qo, kv_indptr, kv_indices[:total_pages], last,
+                                    total_tokens=int(meta[2 * b:3 * b].sum()), causal=is_causal, dtype=dtype)
         ps.seq_lens = list(seq_lens)
         ps.write_store = write_store
 
@@ -420,35 +430,41 @@ class BatchedCacheManager:
         token.  In CUDA-graph mode an existing ``pos_ids`` buffer is rewritten
         in place so captured launches keep their address.
         """
-        eff = label if label is not None else self._single_active_label()
-        ps = self._plan_states.get(eff)
-        if ps is None:
-            ps = self._plan_states[eff] = _PlanState()
-        if pos_ids is not None:
-            src = pos_ids.to(device=self.device, dtype=torch.long)
+        nv = self.enable_nvtx
+        with trace_range(nv, "cache.plan_rope"):
+            eff = label if label is not None else self._single_active_label()
+            ps = self._plan_states.get(eff)
+            if ps is None:
+                ps = self._plan_states[eff] = _PlanState()
+            if pos_ids is not None:
+                with trace_range(nv, "cache.plan_rope.copy_pos_ids"):
+                    src = pos_ids.to(device=self.device, dtype=torch.long)
+                    if self._cuda_graph_mode and ps.pos_ids is not None:
+                        ps.pos_ids[: src.shape[0]].copy_(src, non_blocking=True)
+                    else:
+                        ps.pos_ids = src
+                return
+            b = len(self.request_ids)
+            if len(seq_lens) != b:
+                raise ValueError(f"{len(seq_lens)} seq_lens for {b} requests")
+            with trace_range(nv, "cache.plan_rope.build_pos_ids"):
+                meta = np.empty(2 * b + 1, dtype=np.int32)
+                meta[0] = 0
+                meta[1:b + 1] = np.cumsum(seq_lens, dtype=np.int64)
+                meta[b + 1:] = [self._get_state(rid, eff).position_id_start for rid in self.request_ids]
+            n = int(meta[b]) if b else 0
             if self._cuda_graph_mode and ps.pos_ids is not None:
-                ps.pos_ids[: src.shape[0]].copy_(src, non_blocking=True)
+                if ps.pos_ids.shape[0] < n:
+                    raise ValueError(f"{n} positions do not fit the static pos_ids buffer ({ps.pos_ids.shape[0]})")
+                out = ps.pos_ids
             else:
-                ps.pos_ids = src
-            return
-        b = len(self.request_ids)
-        if len(seq_lens) != b:
-            raise ValueError(f"{len(seq_lens)} seq_lens for {b} requests")
-        meta = np.empty(2 * b + 1, dtype=np.int32)
-        meta[0] = 0
-        meta[1:b + 1] = np.cumsum(seq_lens, dtype=np.int64)
-        meta[b + 1:] = [self._get_state(rid, eff).position_id_start for rid in self.request_ids]
-        n = int(meta[b]) if b else 0
-        if self._cuda_graph_mode and ps.pos_ids is not None:
-            if ps.pos_ids.shape[0] < n:
-                raise ValueError(f"{n} positions do not fit the static pos_ids buffer ({ps.pos_ids.shape[0]})")
-            out = ps.pos_ids
-        else:
-            out = torch.empty(n, dtype=torch.long, device=self.device)
-        if n:
-            dev = self._pack.upload(meta)
-            rope_positions(dev[: b + 1], dev[b + 1:], out, n)
-        ps.pos_ids = out
+                out = torch.empty(n, dtype=torch.long, device=self.device)
+            if n:
+                # the positions are expanded on the device from one small upload
+                with trace_range(nv, "cache.plan_rope.copy_pos_ids"):
+                    dev = self._pack.upload(meta)
+                    rope_positions(dev[: b + 1], dev[b + 1:], out, n)
+            ps.pos_ids = out
 
     def apply_rope(self, q: torch.Tensor, k: torch.Tensor, rotary_dim: int | None = None, interleave: bool = False,
                    rope_scale: float = 1, rope_theta: float = 10000.0, rope_dtype=None, **kwargs):

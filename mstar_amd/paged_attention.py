@@ -32,6 +32,7 @@ import math
 import torch
 
 from . import _lib
+from .trace import trace_range
 
 __all__ = [
     "PagedPrefillWrapper",
@@ -244,21 +245,25 @@ class PagedDecodeWrapper(_FusedRopeAppend):
         else:
             dests = [None, None, None]
         srcs = [paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len]
-        if all(t.device.type == "cpu" for t in srcs):
-            srcs = [t.to(torch.int32) for t in srcs]
-            indptr, indices, last = self._staging.upload(srcs, dev, dests)
-        else:
-            indptr, indices, last = [_as_device_int(t, torch.int32, dev) for t in srcs]
-            if self.use_cuda_graph:
-                for d, s in zip(dests, (indptr, indices, last)):
-                    if d.data_ptr() != s.data_ptr():
-                        d[: s.shape[0]].copy_(s)
-                indptr, indices, last = dests
+        nv = self.enable_nvtx
+        with trace_range(nv, "flashinfer.decode.metadata_h2d"):
+            if all(t.device.type == "cpu" for t in srcs):
+                srcs = [t.to(torch.int32) for t in srcs]
+                indptr, indices, last = self._staging.upload(srcs, dev, dests)
+            else:
+                indptr, indices, last = [_as_device_int(t, torch.int32, dev) for t in srcs]
+                if self.use_cuda_graph:
+                    for d, s in zip(dests, (indptr, indices, last)):
+                        if d.data_ptr() != s.data_ptr():
+                            d[: s.shape[0]].copy_(s)
+                    indptr, indices, last = dests
 
         if kv_cache_locations is not None:
-            loc = kv_cache_locations.to(dev, torch.long, non_blocking=True)
+            with trace_range(nv, "flashinfer.decode.kv_location_h2d"):
+                loc = kv_cache_locations.to(dev, torch.long, non_blocking=True)
             if self.use_cuda_graph:
-                self.kv_cache_locations[:n_req].copy_(loc)
+                with trace_range(nv, "flashinfer.decode.kv_location_copy"):
+                    self.kv_cache_locations[:n_req].copy_(loc)
             else:
                 self.kv_cache_locations = loc
             loc_out = None
@@ -266,16 +271,18 @@ class PagedDecodeWrapper(_FusedRopeAppend):
             if not self.use_cuda_graph:
                 self.kv_cache_locations = torch.empty(n_req, 2, dtype=torch.long, device=dev)
             loc_out = self.kv_cache_locations
-        _lib.check(
-            _lib.lib().mi_decode_plan(
-                None, indptr.data_ptr(), indices.data_ptr(), last.data_ptr(), n_req, self.page_size,
-                self.num_qo_heads, self.num_kv_heads, self.head_dim,
-                loc_out.data_ptr() if loc_out is not None else None,
-                self._workspace.data_ptr(), self._workspace.numel() * self._workspace.element_size(),
-                _lib.stream_ptr(dev),
-            ),
-            "mi_decode_plan",
-        )
+        # the split-KV plan; the write locations (the reference's kv_location_compute) come out of the same launch
+        with trace_range(nv, "flashinfer.decode.plan_inner"):
+            _lib.check(
+                _lib.lib().mi_decode_plan(
+                    None, indptr.data_ptr(), indices.data_ptr(), last.data_ptr(), n_req, self.page_size,
+                    self.num_qo_heads, self.num_kv_heads, self.head_dim,
+                    loc_out.data_ptr() if loc_out is not None else None,
+                    self._workspace.data_ptr(), self._workspace.numel() * self._workspace.element_size(),
+                    _lib.stream_ptr(dev),
+                ),
+                "mi_decode_plan",
+            )
         self._indptr, self._indices, self._last = indptr, indices, last
         self._n_req = n_req
         self.dtype = dtype
