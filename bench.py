@@ -429,6 +429,7 @@ def bench_decode(args, dev) -> dict:
         res["rope"] = bench_rope(q, k, pos_now, args.steps)
         res["rope_append"] = bench_rope_append(cm, q, k, v, pos_now, args.steps)
         res["kv_transfer"] = bench_transfer(kv, args.steps)
+        res["decode_f32_kv"] = bench_f32_decode(dev, args.steps)
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
         res["cpu_baseline"] = cpu_baseline(bt, kv, q, k, v, cm.kv_scales, min_runs=10 if s.name == "c1" else 2)
@@ -580,6 +581,48 @@ def bench_transfer(kv_layer: torch.Tensor, steps: int, pages: int = 32768, host_
         if count_both:
             out[name]["hbm_frac"] = out[name]["GBps"] / HBM_PEAK_GBS
     return out
+
+
+def bench_f32_decode(dev, steps: int) -> dict:
+    """Decode over an fp32 KV pool (the dtype the reference allocates for fp32
+    models, kv_cache_engine.py:104-105) at Pi0.5's attention shape: 8 q / 1 kv
+    head, head_dim 256, page 16; 64 requests with log-uniform [512, 8192]
+    contexts on random pages (seed 5).  Decode kernel time per launch from
+    HIP graph replays of the planned batch; algorithmic bytes as for the
+    bf16 kernel with 4-byte elements."""
+    from mstar_amd.paged_attention import PagedDecodeWrapper
+
+    hq, hkv, d, ps, b = 8, 1, 256, 16, 64
+    g = torch.Generator().manual_seed(5)
+    u = torch.rand(b, generator=g, dtype=torch.float64).numpy()
+    lens = np.rint(np.exp(np.log(512) + u * (np.log(8192) - np.log(512)))).astype(np.int64)
+    pages = (lens + ps - 1) // ps
+    pool = int(pages.sum()) + 64
+    perm = torch.randperm(pool, generator=g).numpy().astype(np.int32)
+    kv_indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    kv_indices = perm[: kv_indptr[-1]]
+    last = (lens - (pages - 1) * ps).astype(np.int32)
+    cache = torch.empty(pool, 2, ps, hkv, d, dtype=torch.float32, device=dev)
+    cache.normal_(generator=torch.Generator(device=dev).manual_seed(5))
+    q = torch.randn(b, hq, d, device=dev)
+    w = PagedDecodeWrapper(torch.empty(256 << 20, dtype=torch.uint8, device=dev), hq, hkv, d, ps, device=dev)
+    w.plan(torch.from_numpy(kv_indptr), torch.from_numpy(kv_indices), torch.from_numpy(last), dtype=torch.float32)
+    out = torch.empty_like(q)
+    args = (q.data_ptr(), _lib.MI_F32, q.stride(0), q.stride(1), _lib.paged_kv_desc(cache), None,
+            w._indptr.data_ptr(), w._indices.data_ptr(), w._last.data_ptr(), b, hq, 0, 1.0 / math.sqrt(d),
+            w._workspace.data_ptr(), w._workspace.numel(), out.data_ptr(), out.stride(0), out.stride(1))
+    L = _lib.lib()
+
+    def attend():
+        for _ in range(4):
+            _lib.check(L.mi_decode_attend(*args, _lib.stream_ptr(dev)), "mi_decode_attend")
+
+    us = _graph_us(attend, dev, steps, per_graph=1) / 4
+    nbytes = int(lens.sum()) * hkv * d * 2 * 4 + b * hq * d * 4 * 2 + 4 * (int(pages.sum()) + 3 * b)
+    return {"kernel": "attend_f32_kernel<256, false>", "what": "fp32 KV decode, 8 q / 1 kv heads, head_dim 256, "
+            f"B={b}, contexts log-uniform [512, 8192] ({int(lens.sum())} KV tokens)", "kernel_us": us,
+            "algorithmic_bytes": nbytes, "GBps": nbytes / (us * 1e-6) / 1e9,
+            "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
 def prefill_flops(bt) -> tuple[int, int]:

@@ -45,7 +45,7 @@ extern "C" {
 /* One layer of the paged KV cache. Strides are in elements. */
 typedef struct mi_paged_kv {
   void* data;           /* element (page 0, K, slot 0, head 0, dim 0) */
-  int32_t dtype;        /* MI_BF16, MI_F16 or MI_FP8_E4M3 */
+  int32_t dtype;        /* MI_BF16, MI_F16, MI_F32 or MI_FP8_E4M3 */
   int32_t page_size;    /* tokens per page */
   int32_t num_kv_heads;
   int32_t head_dim;     /* 64, 128 or 256 */
@@ -145,8 +145,9 @@ int mi_decode_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
  * over the request's kv_len = (npages-1)*page_size + last_page_len tokens
  * (causal alignment to the end of the KV when a request has several query
  * tokens and causal != 0).  q and out: [tokens, num_qo_heads, head_dim] with
- * the given element strides (head_dim contiguous), dtype q_dtype (bf16/fp16).
- * Requests without KV produce zeros.
+ * the given element strides (head_dim contiguous), dtype q_dtype: bf16 or
+ * fp16 (the cache's dtype, or an fp8 cache), or fp32 with an fp32 cache
+ * (attention computed in fp32 throughout).  Requests without KV produce zeros.
  * mi_decode_run = mi_decode_attend (one wavefront per (KV chunk, kv-head):
  * finished rows of unsplit requests, partial (o, lse) of split ones) followed
  * by mi_decode_merge (log-sum-exp merge of the partials); the two halves take
@@ -235,6 +236,7 @@ int mi_kv_append(const mi_paged_kv* kv, const void* k, const void* v, int32_t sr
  * mi_prefill_run replaces FlashInferPrefillWrapper.run (:258-269):
  *   out[t, h] = softmax(sm_scale * q[t,h] . K_r^T) V_r over the request's keys
  *   i <= kv_len - qo_len + j for query j (causal) or all kv_len keys.
+ * q/out dtypes as for mi_decode_run (fp32 with an fp32 cache included).
  * mi_prefill_run = mi_prefill_short (the short-query requests, through the
  * split-KV decode kernel and merge) followed by mi_prefill_tiles (the MFMA
  * tiles of the long-query requests).  The halves take the same arguments and

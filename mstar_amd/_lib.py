@@ -317,8 +317,8 @@ def _build_paged_kv_desc(kv_cache_layer: torch.Tensor, k_scale: torch.Tensor | N
     if kv_cache_layer.stride(4) != 1:
         raise ValueError("kv_cache_layer: head_dim must be contiguous")
     dt = TORCH_TO_MI.get(kv_cache_layer.dtype)
-    if dt is None or dt == MI_F32:
-        raise ValueError(f"unsupported KV cache dtype {kv_cache_layer.dtype} (bf16, fp16 or float8_e4m3fn)")
+    if dt is None:
+        raise ValueError(f"unsupported KV cache dtype {kv_cache_layer.dtype} (bf16, fp16, fp32 or float8_e4m3fn)")
     d = MiPagedKV()
     d.data = kv_cache_layer.data_ptr()
     d.dtype = dt

@@ -12,6 +12,7 @@
 //   any  -> bf16            : via fp32, round-to-nearest-even (NaN -> 0x7FC0)
 //   any  -> f16             : via fp32, round-to-nearest-even
 //   any  -> fp8 e4m3fn      : q = e4m3fn_RNE(clamp(x * (1/scale[h]), -448, 448))
+//   f32 -> f32               : copy;  bf16/f16 -> f32 : exact widening
 #include "mi_common.h"
 
 namespace mi {
@@ -52,8 +53,17 @@ MI_DEVICE void load8(const void* base, int64_t off, float (&x)[8]) {
 
 template <int SRC, int DST>
 MI_DEVICE void move8(const void* src, int64_t soff, uint8_t* dst_row, float inv_scale) {
-  if constexpr (SRC == DST && DST != MI_FP8_E4M3 && DST != MI_F32) {
+  if constexpr (SRC == DST && DST == MI_F32) {  // exact copy, bit patterns kept
+    const uint4* s4 = (const uint4*)((const float*)src + soff);
+    ((uint4*)dst_row)[0] = s4[0];
+    ((uint4*)dst_row)[1] = s4[1];
+  } else if constexpr (SRC == DST && DST != MI_FP8_E4M3) {
     *(uint4*)dst_row = *(const uint4*)((const uint16_t*)src + soff);  // exact copy
+  } else if constexpr (DST == MI_F32) {  // 16-bit source widened exactly
+    float x[8];
+    load8<SRC>(src, soff, x);
+    ((float4*)dst_row)[0] = make_float4(x[0], x[1], x[2], x[3]);
+    ((float4*)dst_row)[1] = make_float4(x[4], x[5], x[6], x[7]);
   } else {
     float x[8];
     load8<SRC>(src, soff, x);
@@ -81,7 +91,7 @@ MI_DEVICE void move8(const void* src, int64_t soff, uint8_t* dst_row, float inv_
 
 template <int SRC, int DST>
 __global__ __launch_bounds__(256) void append_kernel(AppendParams p) {
-  constexpr int ESZ = DST == MI_FP8_E4M3 ? 1 : 2;
+  constexpr int ESZ = DST == MI_FP8_E4M3 ? 1 : DST == MI_F32 ? 4 : 2;
   const int per_token = p.num_kv_heads * (p.head_dim >> 3);
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int i = (int)(gid / per_token);
@@ -112,6 +122,7 @@ static int launch_append_src(const AppendParams& ap, int dst, int grid, hipStrea
     case MI_BF16: hipLaunchKernelGGL((append_kernel<SRC, MI_BF16>), dim3(grid), dim3(256), 0, stream, ap); break;
     case MI_F16: hipLaunchKernelGGL((append_kernel<SRC, MI_F16>), dim3(grid), dim3(256), 0, stream, ap); break;
     case MI_FP8_E4M3: hipLaunchKernelGGL((append_kernel<SRC, MI_FP8_E4M3>), dim3(grid), dim3(256), 0, stream, ap); break;
+    case MI_F32: hipLaunchKernelGGL((append_kernel<SRC, MI_F32>), dim3(grid), dim3(256), 0, stream, ap); break;
     default: return MI_ERR_UNSUPPORTED;
   }
   return MI_OK;
@@ -133,11 +144,11 @@ extern "C" int mi_kv_append(const mi_paged_kv* kv, const void* k, const void* v,
   if (kv->num_kv_heads <= 0 || kv->head_dim <= 0 || kv->page_size <= 0) return MI_ERR_INVALID;
   if (kv->head_dim % 8) return MI_ERR_UNSUPPORTED;
   const int dst = kv->dtype;
-  if (dst != MI_BF16 && dst != MI_F16 && dst != MI_FP8_E4M3) return MI_ERR_UNSUPPORTED;
+  if (dst != MI_BF16 && dst != MI_F16 && dst != MI_FP8_E4M3 && dst != MI_F32) return MI_ERR_UNSUPPORTED;
   if (src_dtype != MI_BF16 && src_dtype != MI_F16 && src_dtype != MI_F32) return MI_ERR_UNSUPPORTED;
   if (dst == MI_FP8_E4M3 && (!kv->k_scale || !kv->v_scale)) return MI_ERR_INVALID;
   // 8-element vector moves need 8-element aligned rows on both sides.
-  const int sesz = src_dtype == MI_F32 ? 4 : 2, desz = dst == MI_FP8_E4M3 ? 1 : 2;
+  const int sesz = src_dtype == MI_F32 ? 4 : 2, desz = dst == MI_FP8_E4M3 ? 1 : dst == MI_F32 ? 4 : 2;
   if ((k_stride_token | k_stride_head | v_stride_token | v_stride_head) % 8) return MI_ERR_INVALID;
   if ((kv->page_stride | kv->kv_stride | kv->token_stride | kv->head_stride) % 8) return MI_ERR_INVALID;
   if (!aligned(k, 8 * sesz) || !aligned(v, 8 * sesz) || !aligned(kv->data, 8 * desz)) return MI_ERR_INVALID;

@@ -116,6 +116,11 @@ struct F16 {
   }
 };
 
+// fp32 output rows (the merge of fp32 attention writes floats).
+struct F32Out {
+  static constexpr int kDtype = MI_F32;
+};
+
 // fp8 e4m3fn pair (selected 16-bit half of `w`) -> packed 16-bit pair of the
 // MFMA type, exact (gfx950 hardware conversion, scale 1.0).
 template <typename MT>

@@ -81,27 +81,6 @@ SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t w
 __global__ __launch_bounds__(1024) void decode_plan_kernel(PlanParams p) { decode_plan_body(p); }
 
 // ---------------------------------------------------------------- decode
-struct DecodeParams {
-  const void* q;
-  int64_t q_stride_tok, q_stride_head;
-  const void* kv;
-  int64_t page_stride, kv_stride, token_stride, head_stride;
-  const float* k_scale;
-  const float* v_scale;
-  const int32_t* qo_indptr;
-  const int32_t* kv_indptr;
-  const int32_t* kv_indices;
-  const int32_t* last_page_len;
-  const int32_t* hdr;
-  const int4* work;
-  const int32_t* chunk_indptr;
-  float* lse_part;
-  float* o_part;
-  void* out;
-  int64_t out_stride_tok, out_stride_head;
-  int32_t num_kv_heads, group, page_size, causal;
-  float scale_log2;
-};
 
 // Per-lane registers of one 16-token tile.
 template <bool FP8, int D>
@@ -524,24 +503,35 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
     }
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  uint16_t* orow = (uint16_t*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
-                   (int64_t)(h * G + g) * p.out_stride_head;
+  const int64_t orow_off = (int64_t)(qo_start + qtok) * p.out_stride_tok + (int64_t)(h * G + g) * p.out_stride_head;
   // store i = r*(VW/4) + j/4 holds d = VW*(4*grp + r) + j .. +3
+  if constexpr (MT::kDtype == MI_F32) {
+    float* orow = (float*)p.out + orow_off;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    uint32_t w[VW / 2];
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int jj = 0; jj < VW / 4; ++jj) {
-      const float4 a = acc[r * (VW / 4) + jj];
-      w[2 * jj] = MT::pack2(a.x * inv, a.y * inv);
-      w[2 * jj + 1] = MT::pack2(a.z * inv, a.w * inv);
-    }
-    uint16_t* dst = orow + VW * (4 * grp + r);
-    if constexpr (VW == 4) {
-      *(uint2*)dst = make_uint2(w[0], w[1]);
-    } else {
+      for (int jj = 0; jj < VW / 4; ++jj) {
+        const float4 a = acc[r * (VW / 4) + jj];
+        *(float4*)(orow + VW * (4 * grp + r) + 4 * jj) = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+      }
+  } else {
+    uint16_t* orow = (uint16_t*)p.out + orow_off;
 #pragma unroll
-      for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+    for (int r = 0; r < 4; ++r) {
+      uint32_t w[VW / 2];
+#pragma unroll
+      for (int jj = 0; jj < VW / 4; ++jj) {
+        const float4 a = acc[r * (VW / 4) + jj];
+        w[2 * jj] = MT::pack2(a.x * inv, a.y * inv);
+        w[2 * jj + 1] = MT::pack2(a.z * inv, a.w * inv);
+      }
+      uint16_t* dst = orow + VW * (4 * grp + r);
+      if constexpr (VW == 4) {
+        *(uint2*)dst = make_uint2(w[0], w[1]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+      }
     }
   }
 }
@@ -605,6 +595,24 @@ static void launch_decode(const DecodeParams& dp, int grid, int batch, int phase
                        batch);
 }
 
+template <int D>
+static void launch_merge_f32(const DecodeParams& dp, int batch, hipStream_t stream) {
+  hipLaunchKernelGGL((merge_kernel<F32Out, D>), dim3((batch * dp.num_kv_heads + 3) / 4), dim3(256), 0, stream, dp,
+                     batch);
+}
+
+int merge_launch(const DecodeParams& dp, int head_dim, int out_dtype, int batch, hipStream_t stream) {
+  if (out_dtype != MI_F32) return MI_ERR_UNSUPPORTED;
+  if (batch <= 0) return MI_OK;
+  switch (head_dim) {
+    case 64: launch_merge_f32<64>(dp, batch, stream); break;
+    case 128: launch_merge_f32<128>(dp, batch, stream); break;
+    case 256: launch_merge_f32<256>(dp, batch, stream); break;
+    default: return MI_ERR_UNSUPPORTED;
+  }
+  return MI_OK;
+}
+
 template <typename MT, bool FP8>
 static int dispatch_d(const DecodeParams& dp, int head_dim, int grid, int batch, int phases, hipStream_t stream) {
   switch (head_dim) {
@@ -631,8 +639,9 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
   if (kv->page_size <= 0) return MI_ERR_INVALID;
   if (kv->page_size % 16 || !supported_head_dim(D)) return MI_ERR_UNSUPPORTED;
   const bool fp8 = kv->dtype == MI_FP8_E4M3;
-  if (q_dtype != MI_BF16 && q_dtype != MI_F16) return MI_ERR_UNSUPPORTED;
+  if (q_dtype != MI_BF16 && q_dtype != MI_F16 && q_dtype != MI_F32) return MI_ERR_UNSUPPORTED;
   if (!fp8 && kv->dtype != q_dtype) return MI_ERR_UNSUPPORTED;
+  if (fp8 && q_dtype == MI_F32) return MI_ERR_UNSUPPORTED;
   if (fp8 && (!kv->k_scale || !kv->v_scale)) return MI_ERR_INVALID;
   const SplitLayout L = split_layout(batch, nkv, D, workspace_bytes - ws_offset);
   if (L.max_chunks <= batch || workspace_bytes < ws_offset + L.total) return MI_ERR_WORKSPACE;
@@ -668,6 +677,14 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
   dp.scale_log2 = sm_scale * 1.4426950408889634f;
   const int grid = (int)((L.max_chunks + 7) / 8 * 8 * (int64_t)nkv);
   int st;
+  if (q_dtype == MI_F32) {  // fp32 q, cache and output
+    st = MI_OK;
+    if (phases & kPhaseAttend) st = f32_attend_launch(dp, D, grid, stream);
+    if (st == MI_OK && (phases & kPhaseMerge)) st = merge_launch(dp, D, MI_F32, batch, stream);
+    if (st != MI_OK) return st;
+    MI_CHECK_LAUNCH();
+    return MI_OK;
+  }
   if (q_dtype == MI_BF16)
     st = fp8 ? dispatch_d<BF16, true>(dp, D, grid, batch, phases, stream)
              : dispatch_d<BF16, false>(dp, D, grid, batch, phases, stream);

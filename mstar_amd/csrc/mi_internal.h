@@ -30,6 +30,40 @@ int decode_plan_params(const int32_t* qo_indptr, const int32_t* kv_indptr, const
 
 enum : int { kPhaseAttend = 1, kPhaseMerge = 2 };
 
+// Arguments of the split-KV decode kernels (decode, merge, and their fp32
+// variants): q/out rows, the KV layer, the packed batch and the plan in the
+// workspace.
+struct DecodeParams {
+  const void* q;
+  int64_t q_stride_tok, q_stride_head;
+  const void* kv;
+  int64_t page_stride, kv_stride, token_stride, head_stride;
+  const float* k_scale;
+  const float* v_scale;
+  const int32_t* qo_indptr;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* last_page_len;
+  const int32_t* hdr;
+  const int4* work;
+  const int32_t* chunk_indptr;
+  float* lse_part;
+  float* o_part;
+  void* out;
+  int64_t out_stride_tok, out_stride_head;
+  int32_t num_kv_heads, group, page_size, causal;
+  float scale_log2;
+};
+
+// fp32 KV (q, cache and output in fp32): the attend phase of a split-KV plan
+// (mi_f32.hip), and the merge with fp32 output (mi_decode.hip).
+int f32_attend_launch(const DecodeParams& dp, int head_dim, int grid, hipStream_t stream);
+int merge_launch(const DecodeParams& dp, int head_dim, int out_dtype, int batch, hipStream_t stream);
+// fp32 ragged prefill over the prefill plan's tile list: one workgroup per
+// (tile, kv-head, 16-row block).
+int f32_prefill_launch(const DecodeParams& dp, const int32_t* tile_hdr, const int2* tiles, int max_tiles,
+                       int tile_rows, int head_dim, hipStream_t stream);
+
 int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int64_t q_stride_head,
                     const mi_paged_kv* kv, const int32_t* qo_indptr, const int32_t* kv_indptr,
                     const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,

@@ -845,8 +845,9 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
   const int G = num_qo_heads / nkv;
   if (G > kShortRows || kv->page_size % 16 || !ok_head_dim(D)) return MI_ERR_UNSUPPORTED;
   const bool fp8 = kv->dtype == MI_FP8_E4M3;
-  if (q_dtype != MI_BF16 && q_dtype != MI_F16) return MI_ERR_UNSUPPORTED;
+  if (q_dtype != MI_BF16 && q_dtype != MI_F16 && q_dtype != MI_F32) return MI_ERR_UNSUPPORTED;
   if (!fp8 && kv->dtype != q_dtype) return MI_ERR_UNSUPPORTED;
+  if (fp8 && q_dtype == MI_F32) return MI_ERR_UNSUPPORTED;
   if (fp8 && (!kv->k_scale || !kv->v_scale)) return MI_ERR_INVALID;
   const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, nkv, D);
   if (workspace_bytes < L.split) return MI_ERR_WORKSPACE;
@@ -859,8 +860,36 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
     if (st != MI_OK) return st;
   }
   if (!(phases & kPhaseTiles)) return MI_OK;
-  // long-query requests: MFMA prefill tiles
   const uint8_t* ws = (const uint8_t*)workspace;
+  if (q_dtype == MI_F32) {  // fp32 KV: one workgroup per (tile, kv-head, 16-row block) of the plan's tiles
+    DecodeParams dp{};
+    dp.q = q;
+    dp.q_stride_tok = q_stride_token;
+    dp.q_stride_head = q_stride_head;
+    dp.kv = kv->data;
+    dp.page_stride = kv->page_stride;
+    dp.kv_stride = kv->kv_stride;
+    dp.token_stride = kv->token_stride;
+    dp.head_stride = kv->head_stride;
+    dp.qo_indptr = qo_indptr;
+    dp.kv_indptr = kv_indptr;
+    dp.kv_indices = kv_indices;
+    dp.last_page_len = last_page_len;
+    dp.out = out;
+    dp.out_stride_tok = out_stride_token;
+    dp.out_stride_head = out_stride_head;
+    dp.num_kv_heads = nkv;
+    dp.group = G;
+    dp.page_size = kv->page_size;
+    dp.causal = causal ? 1 : 0;
+    dp.scale_log2 = sm_scale * 1.4426950408889634f;
+    st = f32_prefill_launch(dp, (const int32_t*)(ws + L.hdr), (const int2*)(ws + L.tiles), L.max_tiles,
+                            pf_rows(D), D, s);
+    if (st != MI_OK) return st;
+    MI_CHECK_LAUNCH();
+    return MI_OK;
+  }
+  // long-query requests: MFMA prefill tiles
   PrefillParams pp;
   pp.q = q;
   pp.q_stride_tok = q_stride_token;

@@ -148,7 +148,16 @@ struct RopeAppendParams {
 // NW 32-bit words of MT elements (2 per word) -> cache elements at dst.
 template <typename MT, int DST, int NW>
 MI_DEVICE void cache_store(uint8_t* dst, const uint32_t* w, float inv_scale) {
-  if constexpr (DST == MT::kDtype) {
+  if constexpr (DST == MI_F32) {  // exact widening of the rounded q/k-dtype values
+    float o[2 * NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      o[2 * i] = MT::to_f32((uint16_t)(w[i] & 0xffffu));
+      o[2 * i + 1] = MT::to_f32((uint16_t)(w[i] >> 16));
+    }
+#pragma unroll
+    for (int i = 0; i < NW / 2; ++i) ((float4*)dst)[i] = make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+  } else if constexpr (DST == MT::kDtype) {
     if constexpr (NW == 2) *(uint2*)dst = make_uint2(w[0], w[1]);
     else *(uint4*)dst = make_uint4(w[0], w[1], w[2], w[3]);
   } else if constexpr (DST == MI_FP8_E4M3) {
@@ -182,7 +191,7 @@ MI_DEVICE void cache_store(uint8_t* dst, const uint32_t* w, float inv_scale) {
 // and every v group, are elements 8g .. 8g+7, copied unrotated.
 template <typename MT, int DST, bool INTERLEAVE>
 __global__ __launch_bounds__(256) void rope_append_kernel(RopeAppendParams a) {
-  constexpr int ESZ = DST == MI_FP8_E4M3 ? 1 : 2;
+  constexpr int ESZ = DST == MI_FP8_E4M3 ? 1 : DST == MI_F32 ? 4 : 2;
   const RopeParams& p = a.r;
   const int groups = a.head_dim >> 3, rgroups = p.rotary_dim >> 3, half = p.rotary_dim >> 1;
   const int hq = p.num_qo_heads, hkv = p.num_kv_heads;
@@ -328,6 +337,7 @@ static int launch_rope_append_src(const RopeAppendParams& a, int dst, int grid, 
     case MI_BF16: launch_rope_append<MT, MI_BF16>(a, grid, s); break;
     case MI_F16: launch_rope_append<MT, MI_F16>(a, grid, s); break;
     case MI_FP8_E4M3: launch_rope_append<MT, MI_FP8_E4M3>(a, grid, s); break;
+    case MI_F32: launch_rope_append<MT, MI_F32>(a, grid, s); break;
     default: return MI_ERR_UNSUPPORTED;
   }
   return MI_OK;
@@ -417,7 +427,7 @@ extern "C" int mi_rope_append(void* q, int64_t q_stride_token, int64_t q_stride_
   if (pos_dtype != MI_I32 && pos_dtype != MI_I64) return MI_ERR_UNSUPPORTED;
   if (rotary_dim <= 0 || rotary_dim > d || rotary_dim % 8 || d % 8) return MI_ERR_UNSUPPORTED;
   const int dst = kv->dtype;
-  if (dst != MI_BF16 && dst != MI_F16 && dst != MI_FP8_E4M3) return MI_ERR_UNSUPPORTED;
+  if (dst != MI_BF16 && dst != MI_F16 && dst != MI_FP8_E4M3 && dst != MI_F32) return MI_ERR_UNSUPPORTED;
   if (dst == MI_FP8_E4M3 && (!kv->k_scale || !kv->v_scale)) return MI_ERR_INVALID;
   if (!(rope_scale > 0.f) || !(rope_theta > 0.f)) return MI_ERR_INVALID;
   // q: 4-element groups (8 elements interleaved); k, v and cache rows: 8-element groups.
@@ -426,7 +436,7 @@ extern "C" int mi_rope_append(void* q, int64_t q_stride_token, int64_t q_stride_
     return MI_ERR_INVALID;
   if ((k_stride_token | k_stride_head | v_stride_token | v_stride_head) % 8) return MI_ERR_INVALID;
   if ((uintptr_t)k % 16 || (uintptr_t)v % 16) return MI_ERR_INVALID;
-  const int desz = dst == MI_FP8_E4M3 ? 1 : 2;
+  const int desz = dst == MI_FP8_E4M3 ? 1 : dst == MI_F32 ? 4 : 2;
   if ((kv->page_stride | kv->kv_stride | kv->token_stride | kv->head_stride) % 8) return MI_ERR_INVALID;
   if ((uintptr_t)kv->data % (8 * desz)) return MI_ERR_INVALID;
   RopeAppendParams a;

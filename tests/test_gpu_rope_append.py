@@ -30,6 +30,8 @@ CASES = [
     (torch.bfloat16, torch.bfloat16, 256, 256, True, None, False, 1),
     (torch.bfloat16, torch.float16, 128, 64, False, L31, True, 1),
     (torch.bfloat16, torch.bfloat16, 64, 32, True, None, True, 1),
+    (torch.bfloat16, torch.float32, 128, 128, False, None, True, 1),
+    (torch.float16, torch.float32, 256, 128, True, L31, False, 2),
 ]
 
 
@@ -176,7 +178,7 @@ def _manager(gpu, kv_dtype, scales=None):
     return BatchedCacheManager(rids, {r: "main" for r in rids}, kv, mgr, bufs, cfg, gpu, kv_scales=scales), cfg
 
 
-@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float32])
 def test_manager_fused_rope_attention_matches_two_calls(gpu, kv_dtype):
     """apply_rope_and_run_attention == apply_rope + run_attention: prefill step then decode steps."""
     scales = None
