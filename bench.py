@@ -429,7 +429,7 @@ def bench_decode(args, dev) -> dict:
         res["rope"] = bench_rope(q, k, pos_now, args.steps)
         res["rope_append"] = bench_rope_append(cm, q, k, v, pos_now, args.steps)
         res["kv_transfer"] = bench_transfer(kv, args.steps)
-        res["decode_f32_kv"] = bench_f32_decode(dev, args.steps)
+        res["decode_side"] = bench_decode_side(dev, args.steps)
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
         res["cpu_baseline"] = cpu_baseline(bt, kv, q, k, v, cm.kv_scales, min_runs=10 if s.name == "c1" else 2)
@@ -583,32 +583,29 @@ def bench_transfer(kv_layer: torch.Tensor, steps: int, pages: int = 32768, host_
     return out
 
 
-def bench_f32_decode(dev, steps: int) -> dict:
-    """Decode over an fp32 KV pool (the dtype the reference allocates for fp32
-    models, kv_cache_engine.py:104-105) at Pi0.5's attention shape: 8 q / 1 kv
-    head, head_dim 256, page 16; 64 requests with log-uniform [512, 8192]
-    contexts on random pages (seed 5).  Decode kernel time per launch from
-    HIP graph replays of the planned batch; algorithmic bytes as for the
-    bf16 kernel with 4-byte elements."""
+def _side_decode(dev, steps: int, hq: int, hkv: int, d: int, lens: np.ndarray, dtype: torch.dtype, seed: int,
+                 pool_pages: int | None = None) -> dict:
+    """Decode kernel time per launch (HIP graph replays of 4 launches of one plan) for
+    one batch of contexts ``lens`` on random pages, page 16, the given dtype."""
     from mstar_amd.paged_attention import PagedDecodeWrapper
 
-    hq, hkv, d, ps, b = 8, 1, 256, 16, 64
-    g = torch.Generator().manual_seed(5)
-    u = torch.rand(b, generator=g, dtype=torch.float64).numpy()
-    lens = np.rint(np.exp(np.log(512) + u * (np.log(8192) - np.log(512)))).astype(np.int64)
+    ps, b = 16, len(lens)
+    g = torch.Generator().manual_seed(seed)
     pages = (lens + ps - 1) // ps
-    pool = int(pages.sum()) + 64
+    pool = pool_pages or int(pages.sum()) + 64
     perm = torch.randperm(pool, generator=g).numpy().astype(np.int32)
     kv_indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
     kv_indices = perm[: kv_indptr[-1]]
     last = (lens - (pages - 1) * ps).astype(np.int32)
-    cache = torch.empty(pool, 2, ps, hkv, d, dtype=torch.float32, device=dev)
-    cache.normal_(generator=torch.Generator(device=dev).manual_seed(5))
-    q = torch.randn(b, hq, d, device=dev)
-    w = PagedDecodeWrapper(torch.empty(256 << 20, dtype=torch.uint8, device=dev), hq, hkv, d, ps, device=dev)
-    w.plan(torch.from_numpy(kv_indptr), torch.from_numpy(kv_indices), torch.from_numpy(last), dtype=torch.float32)
+    cache = torch.empty(pool, 2, ps, hkv, d, dtype=dtype, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    for p0 in range(0, pool, 1 << 14):
+        cache[p0:p0 + (1 << 14)].normal_(generator=gen)
+    q = torch.randn(b, hq, d, device=dev).to(dtype)
+    w = PagedDecodeWrapper(torch.empty(512 << 20, dtype=torch.uint8, device=dev), hq, hkv, d, ps, device=dev)
+    w.plan(torch.from_numpy(kv_indptr), torch.from_numpy(kv_indices), torch.from_numpy(last), dtype=dtype)
     out = torch.empty_like(q)
-    args = (q.data_ptr(), _lib.MI_F32, q.stride(0), q.stride(1), _lib.paged_kv_desc(cache), None,
+    args = (q.data_ptr(), _lib.TORCH_TO_MI[dtype], q.stride(0), q.stride(1), _lib.paged_kv_desc(cache), None,
             w._indptr.data_ptr(), w._indices.data_ptr(), w._last.data_ptr(), b, hq, 0, 1.0 / math.sqrt(d),
             w._workspace.data_ptr(), w._workspace.numel(), out.data_ptr(), out.stride(0), out.stride(1))
     L = _lib.lib()
@@ -617,12 +614,43 @@ def bench_f32_decode(dev, steps: int) -> dict:
         for _ in range(4):
             _lib.check(L.mi_decode_attend(*args, _lib.stream_ptr(dev)), "mi_decode_attend")
 
+    def both():
+        for _ in range(4):
+            _lib.check(L.mi_decode_attend(*args, _lib.stream_ptr(dev)), "mi_decode_attend")
+            _lib.check(L.mi_decode_merge(*args, _lib.stream_ptr(dev)), "mi_decode_merge")
+
     us = _graph_us(attend, dev, steps, per_graph=1) / 4
-    nbytes = int(lens.sum()) * hkv * d * 2 * 4 + b * hq * d * 4 * 2 + 4 * (int(pages.sum()) + 3 * b)
-    return {"kernel": "attend_f32_kernel<256, false>", "what": "fp32 KV decode, 8 q / 1 kv heads, head_dim 256, "
-            f"B={b}, contexts log-uniform [512, 8192] ({int(lens.sum())} KV tokens)", "kernel_us": us,
-            "algorithmic_bytes": nbytes, "GBps": nbytes / (us * 1e-6) / 1e9,
-            "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+    us_dm = _graph_us(both, dev, steps, per_graph=1) / 4
+    esz = cache.element_size()
+    nbytes = int(lens.sum()) * hkv * d * 2 * esz + b * hq * d * q.element_size() * 2 + 4 * (int(pages.sum()) + 3 * b)
+    del cache
+    return {"batch": b, "heads": f"{hq} q / {hkv} kv", "head_dim": d, "kv_dtype": str(dtype).replace("torch.", ""),
+            "kv_tokens": int(lens.sum()), "kernel_us": us, "decode_plus_merge_us": us_dm, "algorithmic_bytes": nbytes,
+            "GBps": nbytes / (us * 1e-6) / 1e9, "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_decode_side(dev, steps: int) -> dict:
+    """Decode at head_dim 256 and over fp32 pools, beside the configuration's step.
+
+    * ``d256_c3_bytes``: the c3 batch (B=256, its contexts) at 16 q / 2 kv heads,
+      head_dim 256: the KV bytes of c3 at twice the head_dim, bf16;
+    * ``pi05_bf16`` / ``pi05_fp32``: Pi0.5's attention shape (8 q / 1 kv head,
+      head_dim 256), 64 requests with log-uniform [512, 8192] contexts (seed 5),
+      bf16 and fp32 pools (the reference allocates fp32 pools for fp32
+      models, kv_cache_engine.py:104-105).
+    Kernel times per launch from HIP graph replays; algorithmic bytes as for
+    the step's decode kernel (KV of every token, q read, o write, indices)."""
+    c3 = S.make_batch("c3")
+    g = torch.Generator().manual_seed(5)
+    u = torch.rand(64, generator=g, dtype=torch.float64).numpy()
+    pi_lens = np.rint(np.exp(np.log(512) + u * (np.log(8192) - np.log(512)))).astype(np.int64)
+    return {
+        "kernel": "decode_kernel<*, false, 256> / attend_f32_kernel<256, false>",
+        "how": "HIP graph replay of 4 decode launches of one plan; decode_plus_merge_us adds the merge launches",
+        "d256_c3_bytes": _side_decode(dev, steps, 16, 2, 256, c3.kv_len.astype(np.int64), torch.bfloat16, 2),
+        "pi05_bf16": _side_decode(dev, steps, 8, 1, 256, pi_lens, torch.bfloat16, 5),
+        "pi05_fp32": _side_decode(dev, steps, 8, 1, 256, pi_lens, torch.float32, 5),
+    }
 
 
 def prefill_flops(bt) -> tuple[int, int]:

@@ -19,14 +19,16 @@
 //             online softmax on S (fp32, exp2 domain)
 //             O^T[D x 16 rows]     += V^T[D x 16 tok] . P^T (v_mfma 16x16x16)
 //           K and V rows are read as whole head_dim rows (16 lanes x 128 bits
-//           per row for D=128) with non-temporal loads, two tiles ahead of the
-//           MFMA work.  The MFMA A operand wants one token per lane%16, which
+//           per row for D=128; every load instruction covers 256 contiguous
+//           bytes of a row, see dim_of) with non-temporal loads, two tiles
+//           ahead of the MFMA work.  The MFMA A operand wants one token per lane%16, which
 //           a register-only layout can only feed with 64-byte row segments
 //           (measured ~15% slower to stream from HBM), so K passes through a
 //           small per-wave LDS buffer: ds_write of the rows, ds_read of the
 //           fragments.  V is transposed in registers (v_perm_b32): output
-//           column d is permuted as d = (D/16)*m + tile, which turns the
-//           transpose into a 4x(D/16) shuffle inside each lane.
+//           row i of output tile m is the dim lane i loaded as its element m
+//           (dim_of), which turns the transpose into a 4x(D/16) shuffle
+//           inside each lane.
 //           The 4 wavefronts' softmax states are merged in LDS; an item that
 //           covers its whole request writes the final output, otherwise a
 //           partial (o, lse).  Partial stores are HBM writes interleaved with
@@ -106,10 +108,10 @@ MI_DEVICE void load_words(uint32_t (&dst)[N], const uint8_t* src) {
     const uint2 t = nt_load8(src);
     dst[0] = t.x;
     dst[1] = t.y;
-  } else {
+  } else {  // 16-byte chunk k of the lane's elements sits 256*k bytes into the row (see dim_of)
 #pragma unroll
     for (int i = 0; i < N; i += 4) {
-      const uint4 t = nt_load16(src + 4 * i);
+      const uint4 t = nt_load16(src + 64 * i);
       dst[i] = t.x;
       dst[i + 1] = t.y;
       dst[i + 2] = t.z;
@@ -124,6 +126,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   constexpr int VW = D / 16;  // V elements per lane per row == output d-tiles
   constexpr int ESZ = FP8 ? 1 : 2;
   constexpr int KRS = D * 2 + 32;  // LDS row stride of the K transpose buffer (8-bank step: conflict-free fragment reads)
+  constexpr int RUN = lane_run(D, ESZ);  // consecutive elements per lane (dim_of)
   constexpr int NS = VW / 4;       // float4 groups per lane per output row segment
   constexpr float kNegInf = -__builtin_inff();
   // LDS: during the tile loop, per-wave K staging (rows arrive as whole
@@ -199,7 +202,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   const uint8_t* kv = (const uint8_t*)p.kv;
   const int64_t head_off = (int64_t)h * p.head_stride * ESZ;
   // per-lane byte offset inside a tile: rows 4*grp + r, elements [VW*col, VW*col + VW)
-  const uint32_t voff0 = (uint32_t)((4 * grp) * p.token_stride + VW * col) * ESZ;
+  const uint32_t voff0 = (uint32_t)((4 * grp) * p.token_stride + RUN * col) * ESZ;
   const uint32_t vrow = (uint32_t)(p.token_stride * ESZ);
   const int64_t kvhalf = p.kv_stride * ESZ;
 
@@ -237,12 +240,13 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int i = 0; i < VW / 2; ++i) w[i] = t.k[r][i];
       }
-      uint8_t* dst = kst + (4 * grp + r) * KRS + VW * 2 * col;
+      uint8_t* dst = kst + (4 * grp + r) * KRS;  // row in natural dim order
       if constexpr (VW == 4) {
-        *(uint2*)dst = make_uint2(w[0], w[1]);
+        *(uint2*)(dst + 2 * dim_of(RUN, col, 0)) = make_uint2(w[0], w[1]);
       } else {
 #pragma unroll
-        for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 4 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+        for (int i = 0; i < VW / 2; i += 4)
+          *(uint4*)(dst + 2 * dim_of(RUN, col, 2 * i)) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
       }
     }
     // ---- S^T = K . Q^T  (A fragment: row col, elements 8*grp + 32*st .. +8)
@@ -396,9 +400,9 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   const float inv = L > 0.f ? vscale / L : 0.f;
   if (!row_valid) return;
   if (nitems_b == 1) {
-    // elements d = VW*(4*grp + wave) + [0, VW) of row col
+    // elements j of output row 4*grp + wave: dims dim_of(RUN, 4*grp + wave, j), row col
     uint16_t* dst = (uint16_t*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
-                    (int64_t)(h * G + g) * p.out_stride_head + VW * (4 * grp + wave);
+                    (int64_t)(h * G + g) * p.out_stride_head;
     uint32_t w[VW / 2];
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
@@ -406,10 +410,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
       w[2 * i + 1] = MT::pack2(o[i].z * inv, o[i].w * inv);
     }
     if constexpr (VW == 4) {
-      *(uint2*)dst = make_uint2(w[0], w[1]);
+      *(uint2*)(dst + dim_of(RUN, 4 * grp + wave, 0)) = make_uint2(w[0], w[1]);
     } else {
 #pragma unroll
-      for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+      for (int i = 0; i < VW / 2; i += 4)
+        *(uint4*)(dst + dim_of(RUN, 4 * grp + wave, 2 * i)) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
     }
   } else {
     // Partial (o, lse) of this item, o in register order: store index
@@ -428,7 +433,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 // decode wavefronts held: row l%16, output elements
 // d = VW*(4*(l/16) + r) + j, read from the register-order partial layout with
 // 64-lane contiguous (cache-line) loads.  Four wavefronts per workgroup.
-template <typename MT, int D>
+template <typename MT, int D, int RUN>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batch) {
   constexpr int VW = D / 16;
   constexpr int NS = 4 * VW / 4;  // float4 stores per lane per partial
@@ -512,7 +517,7 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
 #pragma unroll
       for (int jj = 0; jj < VW / 4; ++jj) {
         const float4 a = acc[r * (VW / 4) + jj];
-        *(float4*)(orow + VW * (4 * grp + r) + 4 * jj) = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+        *(float4*)(orow + dim_of(RUN, 4 * grp + r, 4 * jj)) = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
       }
   } else {
     uint16_t* orow = (uint16_t*)p.out + orow_off;
@@ -525,12 +530,12 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
         w[2 * jj] = MT::pack2(a.x * inv, a.y * inv);
         w[2 * jj + 1] = MT::pack2(a.z * inv, a.w * inv);
       }
-      uint16_t* dst = orow + VW * (4 * grp + r);
       if constexpr (VW == 4) {
-        *(uint2*)dst = make_uint2(w[0], w[1]);
+        *(uint2*)(orow + dim_of(RUN, 4 * grp + r, 0)) = make_uint2(w[0], w[1]);
       } else {
 #pragma unroll
-        for (int i = 0; i < VW / 2; i += 4) *(uint4*)(dst + 2 * i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+        for (int i = 0; i < VW / 2; i += 4)
+          *(uint4*)(orow + dim_of(RUN, 4 * grp + r, 2 * i)) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
       }
     }
   }
@@ -591,14 +596,14 @@ static void launch_decode(const DecodeParams& dp, int grid, int batch, int phase
   if (phases & kPhaseAttend)
     hipLaunchKernelGGL((decode_kernel<MT, FP8, D>), dim3(grid), dim3(256), 0, stream, dp);
   if ((phases & kPhaseMerge) && batch > 0)
-    hipLaunchKernelGGL((merge_kernel<MT, D>), dim3((batch * dp.num_kv_heads + 3) / 4), dim3(256), 0, stream, dp,
-                       batch);
+    hipLaunchKernelGGL((merge_kernel<MT, D, lane_run(D, FP8 ? 1 : 2)>), dim3((batch * dp.num_kv_heads + 3) / 4),
+                       dim3(256), 0, stream, dp, batch);
 }
 
 template <int D>
 static void launch_merge_f32(const DecodeParams& dp, int batch, hipStream_t stream) {
-  hipLaunchKernelGGL((merge_kernel<F32Out, D>), dim3((batch * dp.num_kv_heads + 3) / 4), dim3(256), 0, stream, dp,
-                     batch);
+  hipLaunchKernelGGL((merge_kernel<F32Out, D, lane_run(D, 4)>), dim3((batch * dp.num_kv_heads + 3) / 4), dim3(256),
+                     0, stream, dp, batch);
 }
 
 int merge_launch(const DecodeParams& dp, int head_dim, int out_dtype, int batch, hipStream_t stream) {

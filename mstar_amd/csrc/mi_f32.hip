@@ -29,13 +29,15 @@
 //                                         slot g of step t is key 4g + t, so
 //                                         the B operand is the lane's own
 //                                         probability of key 4g + t; output
-//                                         row i of tile m is dim (D/16)*i + m,
-//                                         so the A operand is one of the
-//                                         lane's own V floats
-// Each lane loads, for its 4 keys 4g..4g+3, the D/16 consecutive floats at
-// dim (D/16)*(lane%16): 16 lanes cover a whole key row with 16-byte loads.
-// K takes the same load layout and passes through a per-wavefront LDS
-// buffer, where each lane reads back its key's D/4-float operand run.
+//                                         row i of tile m is the dim that
+//                                         lane i loaded as its element m, so
+//                                         the A operand is one of the lane's
+//                                         own V floats
+// Each lane loads, for its 4 keys 4g..4g+3, D/16 floats with 16-byte loads,
+// each load instruction covering 256 contiguous bytes of the key row
+// (dim_of in mi_plan.h).  K takes the same load layout and passes through a
+// per-wavefront LDS buffer in natural dim order, where each lane reads back
+// its key's D/4-float operand run.
 #include "mi_common.h"
 #include "mi_internal.h"
 #include "mi_plan.h"
@@ -49,16 +51,16 @@ struct F32Tiles {
 };
 
 template <int D>
-struct F32Regs {  // lane: keys 4*grp + r, dims [(D/16)*col, +D/16)
+struct F32Regs {  // lane: keys 4*grp + r, dims dim_of(lane_run(D, 4), col, j), j < D/16
   float4 k[4][D / 64];
   float4 v[4][D / 64];
 };
 
 template <int N>
-MI_DEVICE void load_f4(float4 (&dst)[N], const uint8_t* src) {
+MI_DEVICE void load_f4(float4 (&dst)[N], const uint8_t* src) {  // float4 i: 256*i bytes into the row (dim_of)
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const uint4 u = nt_load16(src + 16 * i);
+    const uint4 u = nt_load16(src + 256 * i);
     dst[i] = make_float4(bitcast<float>(u.x), bitcast<float>(u.y), bitcast<float>(u.z), bitcast<float>(u.w));
   }
 }
@@ -73,6 +75,7 @@ __global__ __launch_bounds__(256) void attend_f32_kernel(DecodeParams p, F32Tile
   constexpr int NV = VW / 4;      // float4 per lane of a key row
   constexpr int KQ = D / 4;       // S MFMA steps; floats of a lane's Q / K operand run
   constexpr int KRS = D * 4 + 16;  // LDS row stride of the K staging buffer (bytes): rows 4 banks apart
+  constexpr int RUN = lane_run(D, 4);  // consecutive floats per lane (dim_of)
   constexpr float kNegInf = -__builtin_inff();
   constexpr int kStageBytes = 4 * 16 * KRS;
   constexpr int kMergeBytes = 4 * (4 * NV * 64 * 16);
@@ -158,7 +161,7 @@ __global__ __launch_bounds__(256) void attend_f32_kernel(DecodeParams p, F32Tile
 
   const uint8_t* kv = (const uint8_t*)p.kv;
   const int64_t head_off = (int64_t)h * p.head_stride * 4;
-  const uint32_t voff0 = (uint32_t)((4 * grp) * p.token_stride + VW * col) * 4;
+  const uint32_t voff0 = (uint32_t)((4 * grp) * p.token_stride + RUN * col) * 4;
   const uint32_t vrow = (uint32_t)(p.token_stride * 4);
   const int64_t kvhalf = p.kv_stride * 4;
   auto tile_base = [&](int page, int r0) -> const uint8_t* {
@@ -184,9 +187,9 @@ __global__ __launch_bounds__(256) void attend_f32_kernel(DecodeParams p, F32Tile
     // K rows -> LDS (row 4*grp + r, dims [VW*col, +VW)) -> A operand runs
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float4* dst = (float4*)(kst + (4 * grp + r) * KRS + VW * col * 4);
+      float* dst = (float*)(kst + (4 * grp + r) * KRS);  // row in natural dim order
 #pragma unroll
-      for (int i = 0; i < NV; ++i) dst[i] = t.k[r][i];
+      for (int i = 0; i < NV; ++i) *(float4*)(dst + dim_of(RUN, col, 4 * i)) = t.k[r][i];
     }
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     const float4* krun = (const float4*)(kst + col * KRS + KQ * grp * 4);
@@ -307,11 +310,12 @@ __global__ __launch_bounds__(256) void attend_f32_kernel(DecodeParams p, F32Tile
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   if (!row_valid) return;
-  if (nitems_b == 1) {  // dims VW*(4*grp + wave) + [0, VW) of row col
+  if (nitems_b == 1) {  // dims dim_of(RUN, 4*grp + wave, j) of row col
     float* dst = (float*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
-                 (int64_t)(h * G + g) * p.out_stride_head + VW * (4 * grp + wave);
+                 (int64_t)(h * G + g) * p.out_stride_head;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) *(float4*)(dst + 4 * i) = make_float4(o[i].x * inv, o[i].y * inv, o[i].z * inv, o[i].w * inv);
+    for (int i = 0; i < NV; ++i)
+      *(float4*)(dst + dim_of(RUN, 4 * grp + wave, 4 * i)) = make_float4(o[i].x * inv, o[i].y * inv, o[i].z * inv, o[i].w * inv);
   } else {  // partial (o, lse) in the split-KV layout of the decode kernel
     const int64_t unit_idx = (int64_t)(p.chunk_indptr[b] + kidx) * nkv + h;
     float* ob = p.o_part + unit_idx * kRows * D + 4 * lane;
