@@ -42,6 +42,10 @@ __all__ = [
 ]
 
 _MAX_GROUP = 16  # q heads per kv head handled by one MFMA tile
+# A prefill request of at most this many (token, q-head) rows goes to the
+# split-KV decode kernel (mi_prefill_short), a longer one to the MFMA tiles
+# (mi_prefill_tiles); kShortRows in mi_prefill.hip.
+_SHORT_ROWS = 16
 
 
 def _check_heads(num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int) -> None:
@@ -481,6 +485,16 @@ class PagedPrefillWrapper(_FusedRopeAppend):
         self._n_req = n_req
         self._plan_batch = batch
         self._plan_max_tokens = max_tokens
+        # Which of run()'s two launches has work: known on the host for CPU
+        # inputs outside graph mode; otherwise (a captured graph serves any
+        # later mix, device inputs are not read back) both are launched, and
+        # a launch without work exits at once.
+        if on_cpu and not self.use_cuda_graph:
+            rows = torch.diff(qo_indptr.to(torch.int64)) * (self.num_qo_heads // self.num_kv_heads)
+            self._run_short = bool(((rows > 0) & (rows <= _SHORT_ROWS)).any())
+            self._run_tiles = bool((rows > _SHORT_ROWS).any())
+        else:
+            self._run_short = self._run_tiles = True
 
     def run(self, q: torch.Tensor, kv_cache_layer: torch.Tensor, k_scale: torch.Tensor | None = None,
             v_scale: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -508,13 +522,18 @@ class PagedPrefillWrapper(_FusedRopeAppend):
         # short-query requests write disjoint rows: run the HBM-bound decode
         # on a side stream so it overlaps the compute-bound tiles.
         main = torch.cuda.current_stream(q.device)
-        side = self._side
-        side.wait_stream(main)
-        args[-1] = main.cuda_stream
-        _lib.check(_lib.lib().mi_prefill_tiles(*args), "mi_prefill_tiles")
-        args[-1] = side.cuda_stream
-        _lib.check(_lib.lib().mi_prefill_short(*args), "mi_prefill_short")
-        main.wait_stream(side)
+        if self._run_tiles and self._run_short:
+            side = self._side
+            side.wait_stream(main)
+            args[-1] = main.cuda_stream
+            _lib.check(_lib.lib().mi_prefill_tiles(*args), "mi_prefill_tiles")
+            args[-1] = side.cuda_stream
+            _lib.check(_lib.lib().mi_prefill_short(*args), "mi_prefill_short")
+            main.wait_stream(side)
+        elif self._run_tiles or self._run_short:
+            args[-1] = main.cuda_stream
+            fn = "mi_prefill_tiles" if self._run_tiles else "mi_prefill_short"
+            _lib.check(getattr(_lib.lib(), fn)(*args), fn)
         return out
 
     def set_kv_cache(self, kv_cache_layer: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

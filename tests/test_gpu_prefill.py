@@ -108,7 +108,7 @@ MIX_NEW = [40, 1, 120, 0, 300, 2, 5, 3]
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("hq,hkv,d,ps", [(28, 4, 128, 16), (8, 8, 128, 16), (16, 2, 64, 32), (8, 1, 256, 16),
-                                         (32, 2, 128, 64)])
+                                         (32, 2, 128, 64), (16, 2, 256, 32)])
 def test_prefill_ragged_mix(gpu, causal, hq, hkv, d, ps):
     log(f"prefill mix causal={causal} hq={hq} hkv={hkv} d={d} ps={ps}")
     out, ref = _run_prefill(gpu, hq, hkv, d, ps, MIX_KV, MIX_NEW, causal, seed=hq + d)
@@ -117,10 +117,23 @@ def test_prefill_ragged_mix(gpu, causal, hq, hkv, d, ps):
     assert err < TOL
 
 
-def test_prefill_fp16_and_fp8(gpu):
-    out, ref = _run_prefill(gpu, 28, 4, 128, 16, MIX_KV, MIX_NEW, True, seed=3, dtype=torch.float16)
+@pytest.mark.parametrize("kv_lens,new_lens,launches", [([40, 300, 17, 260], [1, 2, 0, 1], "short"),
+                                                      ([40, 300, 700], [40, 3, 300], "tiles")])
+def test_prefill_batch_needing_one_launch(gpu, kv_lens, new_lens, launches):
+    """Batches whose requests all go to one of run()'s two kernels (the other
+    launch is skipped when the host knows it has no work)."""
+    out, ref = _run_prefill(gpu, 28, 4, 128, 16, kv_lens, new_lens, True, seed=11)
+    err = max_abs(out, ref)
+    log(f"prefill {launches}-only batch max_abs={err:.3e}")
+    assert err < TOL
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(28, 4, 128), (8, 1, 256)])
+def test_prefill_fp16_and_fp8(gpu, hq, hkv, d):
+    log(f"prefill fp16 / fp8 hq={hq} hkv={hkv} d={d}")
+    out, ref = _run_prefill(gpu, hq, hkv, d, 16, MIX_KV, MIX_NEW, True, seed=3, dtype=torch.float16)
     assert out.dtype == torch.float16 and max_abs(out, ref) < TOL
-    out, ref = _run_prefill(gpu, 28, 4, 128, 16, MIX_KV, MIX_NEW, True, seed=4, fp8=True)
+    out, ref = _run_prefill(gpu, hq, hkv, d, 16, MIX_KV, MIX_NEW, True, seed=4, fp8=True)
     err = max_abs(out, ref)
     log(f"prefill fp8 max_abs={err:.3e}")
     assert err < TOL_FP8
