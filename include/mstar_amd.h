@@ -148,6 +148,9 @@ int mi_decode_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
  * the given element strides (head_dim contiguous), dtype q_dtype: bf16 or
  * fp16 (the cache's dtype, or an fp8 cache), or fp32 with an fp32 cache
  * (attention computed in fp32 throughout).  Requests without KV produce zeros.
+ * q, out and the KV layer are moved in 16-byte pieces: their bases must be
+ * 16-byte aligned and every element stride a whole number of 16-byte pieces
+ * (MI_ERR_INVALID otherwise; mi_prefill_run checks the same).
  * mi_decode_run = mi_decode_attend (one wavefront per (KV chunk, kv-head):
  * finished rows of unsplit requests, partial (o, lse) of split ones) followed
  * by mi_decode_merge (log-sum-exp merge of the partials); the two halves take

@@ -648,6 +648,10 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
   if (!fp8 && kv->dtype != q_dtype) return MI_ERR_UNSUPPORTED;
   if (fp8 && q_dtype == MI_F32) return MI_ERR_UNSUPPORTED;
   if (fp8 && (!kv->k_scale || !kv->v_scale)) return MI_ERR_INVALID;
+  const int qesz = q_dtype == MI_F32 ? 4 : 2;
+  if (!rows_aligned16(q, q_stride_token, q_stride_head, qesz) ||
+      !rows_aligned16(out, out_stride_token, out_stride_head, qesz) || !kv_aligned16(kv))
+    return MI_ERR_INVALID;
   const SplitLayout L = split_layout(batch, nkv, D, workspace_bytes - ws_offset);
   if (L.max_chunks <= batch || workspace_bytes < ws_offset + L.total) return MI_ERR_WORKSPACE;
   uint8_t* ws = (uint8_t*)workspace + ws_offset;

@@ -30,6 +30,18 @@ int decode_plan_params(const int32_t* qo_indptr, const int32_t* kv_indptr, const
 
 enum : int { kPhaseAttend = 1, kPhaseMerge = 2 };
 
+// The attention kernels move q / out rows and KV rows in 16-byte pieces: a
+// tensor qualifies when its base is 16-byte aligned and each element stride
+// spans a whole number of 16-byte pieces.
+inline bool rows_aligned16(const void* base, int64_t stride_a, int64_t stride_b, int elem_bytes) {
+  return ((uintptr_t)base & 15) == 0 && (stride_a * elem_bytes) % 16 == 0 && (stride_b * elem_bytes) % 16 == 0;
+}
+inline bool kv_aligned16(const mi_paged_kv* kv) {
+  const int esz = kv->dtype == MI_FP8_E4M3 ? 1 : kv->dtype == MI_F32 ? 4 : 2;
+  return rows_aligned16(kv->data, kv->page_stride, kv->kv_stride, esz) &&
+         rows_aligned16(kv->data, kv->token_stride, kv->head_stride, esz);
+}
+
 // Arguments of the split-KV decode kernels (decode, merge, and their fp32
 // variants): q/out rows, the KV layer, the packed batch and the plan in the
 // workspace.

@@ -849,6 +849,10 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
   if (!fp8 && kv->dtype != q_dtype) return MI_ERR_UNSUPPORTED;
   if (fp8 && q_dtype == MI_F32) return MI_ERR_UNSUPPORTED;
   if (fp8 && (!kv->k_scale || !kv->v_scale)) return MI_ERR_INVALID;
+  const int qesz = q_dtype == MI_F32 ? 4 : 2;
+  if (!rows_aligned16(q, q_stride_token, q_stride_head, qesz) ||
+      !rows_aligned16(out, out_stride_token, out_stride_head, qesz) || !kv_aligned16(kv))
+    return MI_ERR_INVALID;
   const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, nkv, D);
   if (workspace_bytes < L.split) return MI_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;

@@ -203,3 +203,33 @@ def test_noalloc_decode_rejects_oversized_batch_on_the_host(L):
                                None) == MI_ERR_INVALID
     assert L.mi_decode_noalloc(p, 0, 4096, 128, ctypes.byref(d), None, p, p, p, 0, 32, 0, 0.1, p, 4096, 128, None,
                                None) == 0
+
+
+def test_attention_entry_points_reject_unaligned_rows_on_the_host(L):
+    """q / out / KV rows that are not 16-byte pieces are rejected before any HIP call."""
+    d = _lib.MiPagedKV()
+    d.data, d.dtype, d.page_size, d.num_kv_heads, d.head_dim = 4096, 0, 16, 4, 128
+    d.page_stride, d.kv_stride, d.token_stride, d.head_stride = 2 * 16 * 4 * 128, 16 * 4 * 128, 4 * 128, 128
+    d.max_pages = 64
+    buf = (ctypes.c_int32 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    base = (ctypes.addressof(buf) + 15) // 16 * 16
+    ws = ctypes.c_void_p(base)
+    ok_q, bad_q = ctypes.c_void_p(base), ctypes.c_void_p(base + 2)
+    for name in ("mi_decode_run", "mi_decode_attend", "mi_decode_merge"):
+        fn = getattr(L, name)
+        # q base off by one element, q token stride of 4 elements, out head stride of 12 elements
+        assert fn(bad_q, 0, 4096, 128, ctypes.byref(d), None, p, p, p, 4, 32, 0, 0.1, ws, 1 << 20, ok_q, 4096,
+                  128, None) == MI_ERR_INVALID
+        assert fn(ok_q, 0, 4, 128, ctypes.byref(d), None, p, p, p, 4, 32, 0, 0.1, ws, 1 << 20, ok_q, 4096, 128,
+                  None) == MI_ERR_INVALID
+        assert fn(ok_q, 0, 4096, 128, ctypes.byref(d), None, p, p, p, 4, 32, 0, 0.1, ws, 1 << 20, ok_q, 4096, 12,
+                  None) == MI_ERR_INVALID
+    bad = _lib.MiPagedKV.from_buffer_copy(d)
+    bad.head_stride = 132  # KV rows of 264 bytes
+    assert L.mi_decode_run(ok_q, 0, 4096, 128, ctypes.byref(bad), None, p, p, p, 4, 32, 0, 0.1, ws, 1 << 20, ok_q,
+                           4096, 128, None) == MI_ERR_INVALID
+    assert L.mi_prefill_run(bad_q, 0, 4096, 128, ctypes.byref(d), p, p, p, p, 4, 64, 32, 1, 0.1, ws, 1 << 20,
+                            ok_q, 4096, 128, None) == MI_ERR_INVALID
+    assert L.mi_prefill_run(ok_q, 0, 4096, 128, ctypes.byref(bad), p, p, p, p, 4, 64, 32, 1, 0.1, ws, 1 << 20,
+                            ok_q, 4096, 128, None) == MI_ERR_INVALID
