@@ -240,6 +240,8 @@ int mi_kv_append(const mi_paged_kv* kv, const void* k, const void* v, int32_t sr
  *   out[t, h] = softmax(sm_scale * q[t,h] . K_r^T) V_r over the request's keys
  *   i <= kv_len - qo_len + j for query j (causal) or all kv_len keys.
  * q/out dtypes as for mi_decode_run (fp32 with an fp32 cache included).
+ * The KV layer's K-to-V offset plus page_size token rows must stay below
+ * 2^31 bytes (MI_ERR_UNSUPPORTED otherwise; M*'s page layout is far below).
  * mi_prefill_run = mi_prefill_short (the short-query requests, through the
  * split-KV decode kernel and merge) followed by mi_prefill_tiles (the MFMA
  * tiles of the long-query requests).  The halves take the same arguments and

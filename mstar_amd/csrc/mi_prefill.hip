@@ -853,6 +853,12 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
   if (!rows_aligned16(q, q_stride_token, q_stride_head, qesz) ||
       !rows_aligned16(out, out_stride_token, out_stride_head, qesz) || !kv_aligned16(kv))
     return MI_ERR_INVALID;
+  // the tile loader keeps a chunk's offset within a page (K/V half, token
+  // row, column) in 32 bits
+  const int64_t kvesz = fp8 ? 1 : kv->dtype == MI_F32 ? 4 : 2;
+  if (kv->kv_stride < 0 || kv->token_stride < 0 ||
+      (kv->kv_stride + (int64_t)kv->page_size * kv->token_stride) * kvesz >= (1LL << 31))
+    return MI_ERR_UNSUPPORTED;
   const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, nkv, D);
   if (workspace_bytes < L.split) return MI_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;

@@ -233,3 +233,9 @@ def test_attention_entry_points_reject_unaligned_rows_on_the_host(L):
                             ok_q, 4096, 128, None) == MI_ERR_INVALID
     assert L.mi_prefill_run(ok_q, 0, 4096, 128, ctypes.byref(bad), p, p, p, p, 4, 64, 32, 1, 0.1, ws, 1 << 20,
                             ok_q, 4096, 128, None) == MI_ERR_INVALID
+    # K and V halves 2^31 bytes apart: beyond the prefill loader's 32-bit in-page offsets
+    far = _lib.MiPagedKV.from_buffer_copy(d)
+    far.kv_stride = 1 << 30
+    far.page_stride = 2 * far.kv_stride
+    assert L.mi_prefill_run(ok_q, 0, 4096, 128, ctypes.byref(far), p, p, p, p, 4, 64, 32, 1, 0.1, ws, 1 << 20,
+                            ok_q, 4096, 128, None) == MI_ERR_UNSUPPORTED
