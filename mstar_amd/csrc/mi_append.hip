@@ -152,7 +152,7 @@ extern "C" int mi_kv_append(const mi_paged_kv* kv, const void* k, const void* v,
   if ((k_stride_token | k_stride_head | v_stride_token | v_stride_head) % 8) return MI_ERR_INVALID;
   if ((kv->page_stride | kv->kv_stride | kv->token_stride | kv->head_stride) % 8) return MI_ERR_INVALID;
   if (!aligned(k, 8 * sesz) || !aligned(v, 8 * sesz) || !aligned(kv->data, 8 * desz)) return MI_ERR_INVALID;
-  AppendParams ap;
+  AppendParams ap{};
   ap.k = k;
   ap.v = v;
   ap.k_stride_tok = k_stride_token;

@@ -582,7 +582,7 @@ int decode_plan_impl(const int32_t* qo_indptr, const int32_t* kv_indptr, const i
                      int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                      int64_t* kv_locations, void* workspace, int64_t workspace_bytes,
                      int64_t ws_offset, hipStream_t stream) {
-  PlanParams pp;
+  PlanParams pp{};
   const int st = decode_plan_params(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
                                     num_kv_heads, head_dim, kv_locations, workspace, workspace_bytes, ws_offset, &pp);
   if (st != MI_OK) return st;
@@ -656,7 +656,7 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
   if (L.max_chunks <= batch || workspace_bytes < ws_offset + L.total) return MI_ERR_WORKSPACE;
   uint8_t* ws = (uint8_t*)workspace + ws_offset;
 
-  DecodeParams dp;
+  DecodeParams dp{};
   dp.q = q;
   dp.q_stride_tok = q_stride_token;
   dp.q_stride_head = q_stride_head;

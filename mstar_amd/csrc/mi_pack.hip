@@ -170,7 +170,7 @@ extern "C" int mi_pack(const int32_t* req_slot, const int32_t* seq_len, const in
                        int32_t page_size, int32_t* qo_indptr, int32_t* kv_indptr, int32_t* kv_indices,
                        int32_t* last_page_len, int64_t* kv_locations, int32_t grid_blocks, void* stream) {
   using namespace mi;
-  PackParams pp;
+  PackParams pp{};
   const int st = pack_params(req_slot, seq_len, new_len, num_pages, batch, block_table, block_table_stride,
                              table_pages, new_pages, page_size, qo_indptr, kv_indptr, kv_indices, last_page_len,
                              kv_locations, grid_blocks, &pp);
@@ -188,12 +188,12 @@ extern "C" int mi_pack_plan(const int32_t* req_slot, const int32_t* seq_len, con
                             int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, void* workspace,
                             int64_t workspace_bytes, void* stream) {
   using namespace mi;
-  PackParams pp;
+  PackParams pp{};
   int st = pack_params(req_slot, seq_len, new_len, num_pages, batch, block_table, block_table_stride, table_pages,
                        new_pages, page_size, qo_indptr, kv_indptr, kv_indices, last_page_len, kv_locations,
                        grid_blocks, &pp);
   if (st != MI_OK) return st;
-  PlanParams pl;
+  PlanParams pl{};
   st = decode_plan_params(nullptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
                           num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, 0, &pl);
   if (st != MI_OK) return st;

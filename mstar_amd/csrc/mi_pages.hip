@@ -45,7 +45,7 @@ extern "C" int mi_copy_pages(void* pool, int64_t layer_stride_bytes, int32_t num
   if ((uintptr_t)pool % 16 || layer_stride_bytes % 16 || page_stride_bytes % 16 || page_bytes % 16 ||
       page_bytes > page_stride_bytes)
     return MI_ERR_INVALID;
-  CopyPagesParams p;
+  CopyPagesParams p{};
   p.pool = (uint8_t*)pool;
   p.layer_stride = layer_stride_bytes;
   p.page_stride = page_stride_bytes;
@@ -254,7 +254,7 @@ extern "C" int mi_kv_copy_tokens(const mi_kv_pool* src, const mi_kv_pool* dst, c
                                  const int32_t* dst_pages, const int32_t* token_start, const int32_t* token_end,
                                  int32_t num_records, int32_t layer_begin, int32_t layer_end, void* stream) {
   using namespace mi;
-  SegParams p;
+  SegParams p{};
   if (const int rc = seg_common(src, token_start, token_end, num_records, layer_begin, layer_end, p)) return rc;
   if (const int rc = seg_pool_check(dst, layer_end)) return rc;
   if (dst->token_stride != src->token_stride || dst->page_size != src->page_size) return MI_ERR_INVALID;
@@ -272,7 +272,7 @@ extern "C" int mi_kv_wire_pack(const mi_kv_pool* pool, const int32_t* pages, con
                                int32_t layer_begin, int32_t layer_end, void* wire, int64_t wire_bytes,
                                void* stream) {
   using namespace mi;
-  SegParams p;
+  SegParams p{};
   if (const int rc = seg_common(pool, token_start, token_end, num_records, layer_begin, layer_end, p)) return rc;
   if (token_start && !row_offset) return MI_ERR_INVALID;
   if (num_records == 0 || layer_end == layer_begin) return MI_OK;
@@ -290,7 +290,7 @@ extern "C" int mi_kv_wire_unpack(const void* wire, int64_t wire_bytes, const mi_
                                  const int64_t* row_offset, int32_t num_records, int32_t layer_begin,
                                  int32_t layer_end, void* stream) {
   using namespace mi;
-  SegParams p;
+  SegParams p{};
   if (const int rc = seg_common(pool, token_start, token_end, num_records, layer_begin, layer_end, p)) return rc;
   if (token_start && !row_offset) return MI_ERR_INVALID;
   if (num_records == 0 || layer_end == layer_begin) return MI_OK;

@@ -790,7 +790,7 @@ extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
   const PrefillLayout L = prefill_layout(batch, max_qo_tokens, G, num_kv_heads, head_dim);
   if (workspace_bytes < L.split) return MI_ERR_WORKSPACE;
   uint8_t* ws = (uint8_t*)workspace;
-  PlanParams d;
+  PlanParams d{};
   const int st = decode_plan_params(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
                                     num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, L.split, &d);
   if (st != MI_OK) return st;
@@ -900,7 +900,7 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
     return MI_OK;
   }
   // long-query requests: MFMA prefill tiles
-  PrefillParams pp;
+  PrefillParams pp{};
   pp.q = q;
   pp.q_stride_tok = q_stride_token;
   pp.q_stride_head = q_stride_head;

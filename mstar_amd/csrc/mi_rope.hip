@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
 // dtype before the cache conversion, so the cache holds what
 // rope-then-append writes, bit for bit.
 struct RopeAppendParams {
-  RopeParams r;
+  RopeParams r{};
   const void* v;
   int64_t v_stride_tok, v_stride_head;
   void* cache;
@@ -376,7 +376,7 @@ extern "C" int mi_rope_apply(void* q, int64_t q_stride_token, int64_t q_stride_h
   if ((num_qo_heads > 0 && ((uintptr_t)q % (2 * align) || q_stride_token % align || q_stride_head % align)) ||
       (num_kv_heads > 0 && ((uintptr_t)k % (2 * align) || k_stride_token % align || k_stride_head % align)))
     return MI_ERR_INVALID;
-  RopeParams p;
+  RopeParams p{};
   p.q = q;
   p.k = k;
   p.q_stride_tok = q_stride_token;
@@ -439,7 +439,7 @@ extern "C" int mi_rope_append(void* q, int64_t q_stride_token, int64_t q_stride_
   const int desz = dst == MI_FP8_E4M3 ? 1 : dst == MI_F32 ? 4 : 2;
   if ((kv->page_stride | kv->kv_stride | kv->token_stride | kv->head_stride) % 8) return MI_ERR_INVALID;
   if ((uintptr_t)kv->data % (8 * desz)) return MI_ERR_INVALID;
-  RopeAppendParams a;
+  RopeAppendParams a{};
   RopeParams& p = a.r;
   p.q = q;
   p.k = k;
