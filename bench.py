@@ -761,7 +761,49 @@ def bench_prefill(args, dev) -> dict:
     if not args.no_extra:
         res["prefill_head_dim_256"] = bench_prefill_d256(dev, args.steps)
         res["prefill_fp8_kv"] = bench_prefill_fp8(w, q, layer, s, dev, args.steps, long_f)
+        res["prefill_vs_torch_sdpa"] = bench_prefill_vs_sdpa(dev, min(args.steps, 10))
     return res
+
+
+def bench_prefill_vs_sdpa(dev, steps: int) -> dict:
+    """A dense causal GQA prefill (8 sequences of 4096 tokens, 28 q / 4 kv heads,
+    head_dim 128, bf16) through PyTorch-ROCm's fused attention
+    (``scaled_dot_product_attention(..., enable_gqa=True)``) and through this
+    build's paged prefill (8 requests of 4096 new tokens on random pages): the
+    same algorithmic flops, HIP events around each call."""
+    import torch.nn.functional as F
+    from mstar_amd.paged_attention import PagedPrefillWrapper
+
+    b, n, hq, hkv, d, ps = 8, 4096, 28, 4, 128, 16
+    flops = 4 * b * hq * d * (n * (n + 1) // 2)
+    g = torch.Generator(device=dev).manual_seed(9)
+    q = torch.randn(b, hq, n, d, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(b, hkv, n, d, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(b, hkv, n, d, device=dev, generator=g).to(torch.bfloat16)
+    pages = n // ps
+    pool = b * pages + 8
+    perm = torch.randperm(pool, generator=torch.Generator().manual_seed(9)).numpy().astype(np.int32)
+    kv_indptr = (np.arange(b + 1) * pages).astype(np.int32)
+    last = np.full(b, ps, np.int32)
+    qo = (np.arange(b + 1) * n).astype(np.int32)
+    cache = torch.empty(pool, 2, ps, hkv, d, device=dev, dtype=torch.bfloat16)
+    w = PagedPrefillWrapper(torch.empty(512 << 20, dtype=torch.uint8, device=dev), hq, hkv, d, ps, device=dev)
+    w.plan(*(torch.from_numpy(a) for a in (qo, kv_indptr, perm[: b * pages], last)), causal=True)
+    qp = q.transpose(1, 2).reshape(b * n, hq, d).contiguous()
+    w.set_kv_cache(cache, k.transpose(1, 2).reshape(b * n, hkv, d).contiguous(),
+                   v.transpose(1, 2).reshape(b * n, hkv, d).contiguous())
+    sdpa = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+    ours = lambda: w.run(qp, cache)
+    for _ in range(2):
+        sdpa()
+        ours()
+    us_sdpa, us_ours = _run_us(sdpa, steps), _run_us(ours, steps)
+    diff = (ours().float() - sdpa().transpose(1, 2).reshape(b * n, hq, d).float()).abs().max().item()
+    return {"shape": f"{b} x {n} tokens, {hq} q / {hkv} kv heads, head_dim {d}, causal, bf16",
+            "algorithmic_flops": flops,
+            "torch_sdpa_us": us_sdpa, "torch_sdpa_frac": flops / us_sdpa / 1e6 / MFMA_BF16_PEAK_TFLOPS,
+            "paged_prefill_us": us_ours, "paged_prefill_frac": flops / us_ours / 1e6 / MFMA_BF16_PEAK_TFLOPS,
+            "max_abs_diff": diff}
 
 
 def _run_us(fn, steps: int) -> float:
