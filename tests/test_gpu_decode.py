@@ -96,7 +96,8 @@ def test_decode_long_context_split(gpu, name, nreq):
 @pytest.mark.parametrize(
     "hq,hkv,d,ps",
     [(8, 1, 256, 16), (8, 2, 64, 16), (24, 8, 128, 32), (28, 4, 128, 16), (16, 1, 128, 128), (4, 4, 128, 16),
-     (32, 2, 64, 64), (8, 2, 128, 256), (32, 4, 128, 48), (8, 1, 256, 80)],
+     (32, 2, 64, 64), (8, 2, 128, 256), (32, 4, 128, 48), (8, 1, 256, 80), (20, 4, 128, 16),
+     (48, 4, 128, 32)],
 )
 def test_decode_shapes(gpu, hq, hkv, d, ps):
     lens = [1, 15, 16, 17, 255, 256, 257, 1000, 3001]

@@ -109,7 +109,7 @@ MIX_NEW = [40, 1, 120, 0, 300, 2, 5, 3]
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("hq,hkv,d,ps", [(28, 4, 128, 16), (8, 8, 128, 16), (16, 2, 64, 32), (8, 1, 256, 16),
                                          (32, 2, 128, 64), (16, 2, 256, 32), (8, 2, 128, 128), (28, 4, 128, 48),
-                                         (8, 1, 256, 80)])
+                                         (8, 1, 256, 80), (20, 4, 128, 16), (48, 4, 64, 32)])
 def test_prefill_ragged_mix(gpu, causal, hq, hkv, d, ps):
     log(f"prefill mix causal={causal} hq={hq} hkv={hkv} d={d} ps={ps}")
     out, ref = _run_prefill(gpu, hq, hkv, d, ps, MIX_KV, MIX_NEW, causal, seed=hq + d)
