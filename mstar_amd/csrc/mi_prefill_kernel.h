@@ -169,9 +169,13 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   }
   const int key_cap = np * ps - 16;  // last 16-row group inside the request's pages
   int c0 = 0;  // first page of the page ids staged in LDS
-  // NB register buffers (even): tile t+NB is loaded while tile t is computed
-  // Three register buffers: tile i is loaded three steps before it is stored
-  constexpr int NB = 3;
+  // NB register buffers: tile X is loaded into buffer (X - t0) % NB, NB steps
+  // before the step that stores it to LDS.  Three; two at head_dim 256, whose
+  // tiles take four chunks per thread, so that its deeper LDS read-ahead (KLA,
+  // VLA below) fits the register file.  The step loop is unrolled over
+  // lcm(3 LDS stages, NB) steps.
+  constexpr int NB = D > 128 ? 2 : 3;
+  constexpr int UNR = NB == 2 ? 6 : 3;
   uint4 rr[NB][NL];
   // A tile's loads in two parts: the page ids (LDS reads) and the global
   // loads, so a step can read its page ids early and issue the loads later.
@@ -272,15 +276,19 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       for (int js = 0; js < 2; ++js)
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) s[rg][js] = MT::mma_16x16x32(a[js][st], qf[rg][st], s[rg][js]);
-    // K fragment reads of slice st+1 ahead of the MFMAs of slice st (fewer
-    // live fragment registers; c4 592 -> 586 us against all reads first).
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    // K fragment reads KLA slices ahead of the MFMAs that use them: one at
+    // head_dim 128 and below (four MFMAs per slice cover the LDS latency; c4
+    // 592 -> 586 us against all reads first), two at head_dim 256, whose
+    // slices feed two MFMAs each (with VLA: 1693 -> 1540 us on the bench's
+    // head_dim 256 batch).
+    constexpr int KLA = D > 128 ? 2 : 1;
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * KLA, 0);
 #pragma unroll
-    for (int st = 1; st < KS; ++st) {
+    for (int st = KLA; st < KS; ++st) {
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 2 * RG, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2 * RG, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * RG * KLA, 0);
   };
   // Softmax in two parts: sm_max masks (tail tiles only), takes the row max
   // and raises the running max when needed (a rare branch); sm_exp forms
@@ -365,14 +373,15 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     for (int jj = 0; jj < VW; ++jj)
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg) acc[rg][jj] = MT::mma_16x16x32(a[jj], pb[rg], acc[rg][jj]);
-    if constexpr (!VPRE) {  // fragments read just before: the reads of tile jj+1 ahead of its MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    if constexpr (!VPRE) {  // fragments read just before use: VLA output tiles ahead of their MFMAs
+      constexpr int VLA = 4;
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * VLA, 0);
 #pragma unroll
-      for (int jj = 1; jj < VW; ++jj) {
+      for (int jj = VLA; jj < VW; ++jj) {
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, RG, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, RG, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, RG * VLA, 0);
     }
   };
   // Ping-pong: the two wavefronts that share a SIMD (one of waves {0,2,5,7},
@@ -395,13 +404,12 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     const int tl = t1 - 1;
     // Three-stage LDS ring: in step T both groups read V of tile T-1 (P.V)
     // and K of tile T (scores), and tile T+1 is stored into the stage tile
-    // T-2 used.  Register buffer j holds the tiles t0 + j (mod 3), loaded
-    // three steps before they are stored.
+    // T-2 used; the register buffer it came from then takes tile T+1+NB.
     const int n = t1 - t0;
 #pragma unroll
     for (int u = 0; u < NB; ++u) load_tile(min(t0 + u, tl), rr[u]);
     store_tile(t0, rr[0], 0);
-    load_tile(min(t0 + 3, tl), rr[0]);
+    load_tile(min(t0 + NB, tl), rr[0]);
     __syncthreads();
     f32x4 sc[RG][2];
     uint4 pbk[RG];
@@ -414,29 +422,29 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       sm_exp(sc, pbk);
     }
     store_tile(min(t0 + 1, tl), rr[1], 1);
-    load_tile(min(t0 + 4, tl), rr[1]);
+    load_tile(min(t0 + 1 + NB, tl), rr[1]);
     __syncthreads();
     // steps 1 .. n-1
-    for (int i = 1; i < n; i += 3) {
+    for (int i = 1; i < n; i += UNR) {
 #pragma unroll
-      for (int u = 0; u < 3; ++u) {
+      for (int u = 0; u < UNR; ++u) {
         const int ii = i + u;
         if (ii >= n) break;
         const int T = t0 + ii;
         // Tile T+1 goes into the stage tile T-2 used, which no wave reads in
-        // this step; each group stores it (and issues the loads of tile T+4)
+        // this step; each group stores it (and issues the loads of tile T+1+NB)
         // in its vector half, under the other group's MFMA work.
         int pg4[NL];
-        tile_pages(min(T + 4, tl), pg4);
+        tile_pages(min(T + 1 + NB, tl), pg4);
         // Each group's vector half runs at raised wave priority, so its softmax
         // issues ahead of the partner's MFMA stream on the shared SIMD
         // (c4 583 -> 580 us, head_dim 256 1794 -> 1747 us).
         if (grp_a) {
           __builtin_amdgcn_s_setprio(1);
-          store_tile(min(T + 1, tl), rr[(u + 2) % 3], (u + 2) % 3);
+          store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
           sm_max(T - 1, sc);
           sm_exp(sc, pbk);
-          load_tile_at(min(T + 4, tl), pg4, rr[(u + 2) % 3]);
+          load_tile_at(min(T + 1 + NB, tl), pg4, rr[(u + 2) % NB]);
           __builtin_amdgcn_s_setprio(0);
         }
         // scores of tile T first (group B's softmax waits on them), then P.V of
@@ -447,8 +455,8 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         if constexpr (VPRE) vfrag((u + 1) % 3, va);
         if (!grp_a) {
           __builtin_amdgcn_s_setprio(1);
-          store_tile(min(T + 1, tl), rr[(u + 2) % 3], (u + 2) % 3);
-          load_tile_at(min(T + 4, tl), pg4, rr[(u + 2) % 3]);
+          store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
+          load_tile_at(min(T + 1 + NB, tl), pg4, rr[(u + 2) % NB]);
           sm_max(T, sc);
           sm_exp(sc, pbk);
           __builtin_amdgcn_s_setprio(0);
