@@ -170,12 +170,13 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   const int key_cap = np * ps - 16;  // last 16-row group inside the request's pages
   int c0 = 0;  // first page of the page ids staged in LDS
   // NB register buffers: tile X is loaded into buffer (X - t0) % NB, NB steps
-  // before the step that stores it to LDS.  Three; two at head_dim 256, whose
-  // tiles take four chunks per thread, so that its deeper LDS read-ahead (KLA,
-  // VLA below) fits the register file.  The step loop is unrolled over
-  // lcm(3 LDS stages, NB) steps.
-  constexpr int NB = D > 128 ? 2 : 3;
-  constexpr int UNR = NB == 2 ? 6 : 3;
+  // before the step that stores it to LDS.  Two: with three (loads one step
+  // further ahead) the c4 batch ran 1.5-2.5% slower at head_dim 128 (225 vs
+  // 217 VGPRs), and head_dim 256 needs the registers for its deeper LDS
+  // read-ahead (KLA, VLA below).  The step loop is unrolled over lcm(3 LDS
+  // stages, NB) steps.
+  constexpr int NB = 2;
+  constexpr int UNR = 6;
   uint4 rr[NB][NL];
   // A tile's loads in two parts: the page ids (LDS reads) and the global
   // loads, so a step can read its page ids early and issue the loads later.
