@@ -50,12 +50,18 @@ constexpr int kMinChunkTokens = 1024;  // never split a request finer than this 
 // wave units fill 256 CUs x 2 resident workgroups about twice; with the
 // longest-first work order the drain tail stays short while few requests
 // need partials (measured on c3: 4096 -> 545 us, 8192 -> 558 us,
-// 16384 -> 586 us).
+// 16384 -> 586 us; 2048 and 1024 units: 538-540 and 609 us).
 constexpr int32_t kDecodeTargetUnits = 4096;
+// head_dim 256: one resident workgroup per CU and twice the bytes per token,
+// so fewer and longer items: c3's contexts at 16 q / 2 kv heads 536 -> 507 us
+// (1536 units: 524 us); smaller batches, whose items kMinChunkTokens bounds
+// (Pi0.5's 8 q / 1 kv), are unchanged.
+constexpr int32_t kDecodeTargetUnitsWide = 1024;
 
 SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t ws_avail) {
   SplitLayout L;
-  int32_t target = kDecodeTargetUnits / (4 * (nkv > 0 ? nkv : 1));  // 4 waves per item
+  const int32_t units = head_dim > 128 ? kDecodeTargetUnitsWide : kDecodeTargetUnits;
+  int32_t target = units / (4 * (nkv > 0 ? nkv : 1));  // 4 waves per item
   if (target < 16) target = 16;
   int64_t max_chunks = (int64_t)target + batch;
   if (ws_avail >= 0) {  // fewer, longer chunks when the caller's workspace is smaller
