@@ -58,10 +58,12 @@ constexpr int32_t kDecodeTargetUnits = 4096;
 // (Pi0.5's 8 q / 1 kv), are unchanged.
 constexpr int32_t kDecodeTargetUnitsWide = 1024;
 
-SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t ws_avail) {
+SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t ws_avail, bool pair) {
   SplitLayout L;
-  const int32_t units = head_dim > 128 ? kDecodeTargetUnitsWide : kDecodeTargetUnits;
-  int32_t target = units / (4 * (nkv > 0 ? nkv : 1));  // 4 waves per item
+  // a paired plan is a head_dim 256 plan over half the kv-heads
+  const int32_t tnkv = pair ? nkv / 2 : nkv, thd = pair ? 2 * head_dim : head_dim;
+  const int32_t units = thd > 128 ? kDecodeTargetUnitsWide : kDecodeTargetUnits;
+  int32_t target = units / (4 * (tnkv > 0 ? tnkv : 1));  // 4 waves per item
   if (target < 16) target = 16;
   int64_t max_chunks = (int64_t)target + batch;
   if (ws_avail >= 0) {  // fewer, longer chunks when the caller's workspace is smaller
@@ -126,8 +128,12 @@ MI_DEVICE void load_words(uint32_t (&dst)[N], const uint8_t* src) {
   }
 }
 
-template <typename MT, bool FP8, int D>
+// PAIR (D = 256): two adjacent head_dim 128 kv-heads read as one 256-element
+// row; p.num_kv_heads counts the pairs, p.group is the real group size, query
+// row col belongs to kv-head 2h + (col >= group) (see pair_heads).
+template <typename MT, bool FP8, int D, bool PAIR = false>
 __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
+  static_assert(!PAIR || D == 256, "paired kv-heads form 256-element rows");
   constexpr int KS = D / 32;  // MFMA k-steps over head_dim for S
   constexpr int VW = D / 16;  // V elements per lane per row == output d-tiles
   constexpr int ESZ = FP8 ? 1 : 2;
@@ -168,7 +174,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     qo_len = p.qo_indptr[b + 1] - qo_start;
   }
   const int G = p.group;
-  const int rows = min(qo_len * G, kRows);
+  const int rows = min((PAIR ? 2 : 1) * qo_len * G, kRows);
   const int item_tok0 = pg0 * ps;
   const int item_tok1 = min(pg1 * ps, kv_len);
   const int item_tiles = item_tok1 > item_tok0 ? (item_tok1 - item_tok0 + 15) >> 4 : 0;
@@ -180,8 +186,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 
   const int col = lane & 15;  // query row handled in MFMA column `col`
   const int grp = lane >> 4;  // 0..3
-  const int qtok = col / G;
-  const int g = col - qtok * G;
+  const int half = PAIR && col >= qo_len * G ? 1 : 0;  // PAIR: which head of the pair
+  const int rcol = col - half * qo_len * G;
+  const int hq = PAIR ? 2 * h + half : h;  // the row's kv-head
+  const int qtok = rcol / G;
+  const int g = rcol - qtok * G;
   const bool row_valid = col < rows;
   // Keys this row may attend: [0, lim]  (causal: aligned to the end of the KV).
   int lim = p.causal ? (kv_len - qo_len + qtok) : (kv_len - 1);
@@ -193,15 +202,19 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   uint4 qf[KS];
   {
     const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(qo_start + qtok) * p.q_stride_tok +
-                           (int64_t)(h * G + g) * p.q_stride_head;
+                           (int64_t)(hq * G + g) * p.q_stride_head;
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      qf[s] = row_valid ? *(const uint4*)(qrow + 32 * s + 8 * grp) : make_uint4(0, 0, 0, 0);
+    for (int s = 0; s < KS; ++s) {
+      // PAIR: the row's 128 elements sit in its half of the 256, zeros in the other
+      const int sr = PAIR ? s - (KS / 2) * half : s;
+      const bool in = PAIR ? (sr >= 0 && sr < KS / 2) : true;
+      qf[s] = row_valid && in ? *(const uint4*)(qrow + 32 * sr + 8 * grp) : make_uint4(0, 0, 0, 0);
+    }
   }
   float kscale = 1.0f, vscale = 1.0f;
   if constexpr (FP8) {
-    kscale = p.k_scale[h];
-    vscale = p.v_scale[h];
+    kscale = p.k_scale[hq];
+    vscale = p.v_scale[hq];
   }
   const float sl2 = p.scale_log2 * kscale;
 
@@ -408,7 +421,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   if (nitems_b == 1) {
     // elements j of output row 4*grp + wave: dims dim_of(RUN, 4*grp + wave, j), row col
     uint16_t* dst = (uint16_t*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
-                    (int64_t)(h * G + g) * p.out_stride_head;
+                    (int64_t)(hq * G + g) * p.out_stride_head;
     uint32_t w[VW / 2];
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
@@ -419,8 +432,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
       *(uint2*)(dst + dim_of(RUN, 4 * grp + wave, 0)) = make_uint2(w[0], w[1]);
     } else {
 #pragma unroll
-      for (int i = 0; i < VW / 2; i += 4)
-        *(uint4*)(dst + dim_of(RUN, 4 * grp + wave, 2 * i)) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+      for (int i = 0; i < VW / 2; i += 4) {
+        const int d0 = dim_of(RUN, 4 * grp + wave, 2 * i);  // 8 consecutive elements
+        if (PAIR && (d0 >= D / 2) != (half == 1)) continue;  // the other head's half
+        *(uint4*)(dst + d0 - (PAIR ? (D / 2) * half : 0)) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+      }
     }
   } else {
     // Partial (o, lse) of this item, o in register order: store index
@@ -439,8 +455,9 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 // decode wavefronts held: row l%16, output elements
 // d = VW*(4*(l/16) + r) + j, read from the register-order partial layout with
 // 64-lane contiguous (cache-line) loads.  Four wavefronts per workgroup.
-template <typename MT, int D, int RUN>
+template <typename MT, int D, int RUN, bool PAIR = false>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batch) {
+  static_assert(!PAIR || D == 256, "paired kv-heads form 256-element rows");
   constexpr int VW = D / 16;
   constexpr int NS = 4 * VW / 4;  // float4 stores per lane per partial
   constexpr float kNegInf = -__builtin_inff();
@@ -458,12 +475,15 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
     qo_len = p.qo_indptr[b + 1] - qo_start;
   }
   const int G = p.group;
-  if (qo_len * G > kRows) return;  // long-query request: written by the prefill kernel
-  const int rows = qo_len * G;
+  const int rows = (PAIR ? 2 : 1) * qo_len * G;
+  if (rows > kRows) return;  // long-query request: written by the prefill kernel
   const int lane = lane_id();
   const int col = lane & 15, grp = lane >> 4;
   if (col >= rows) return;
-  const int qtok = col / G, g = col - qtok * G;
+  const int half = PAIR && col >= qo_len * G ? 1 : 0;
+  const int rcol = col - half * qo_len * G;
+  const int hq = PAIR ? 2 * h + half : h;
+  const int qtok = rcol / G, g = rcol - qtok * G;
   float4 acc[NS];
 #pragma unroll
   for (int i = 0; i < NS; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -514,7 +534,7 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
     }
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  const int64_t orow_off = (int64_t)(qo_start + qtok) * p.out_stride_tok + (int64_t)(h * G + g) * p.out_stride_head;
+  const int64_t orow_off = (int64_t)(qo_start + qtok) * p.out_stride_tok + (int64_t)(hq * G + g) * p.out_stride_head;
   // store i = r*(VW/4) + j/4 holds d = VW*(4*grp + r) + j .. +3
   if constexpr (MT::kDtype == MI_F32) {
     float* orow = (float*)p.out + orow_off;
@@ -540,8 +560,11 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
         *(uint2*)(orow + dim_of(RUN, 4 * grp + r, 0)) = make_uint2(w[0], w[1]);
       } else {
 #pragma unroll
-        for (int i = 0; i < VW / 2; i += 4)
-          *(uint4*)(orow + dim_of(RUN, 4 * grp + r, 2 * i)) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+        for (int i = 0; i < VW / 2; i += 4) {
+          const int d0 = dim_of(RUN, 4 * grp + r, 2 * i);  // 8 consecutive elements
+          if (PAIR && (d0 >= D / 2) != (half == 1)) continue;  // the other head's half
+          *(uint4*)(orow + d0 - (PAIR ? (D / 2) * half : 0)) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+        }
       }
     }
   }
@@ -562,7 +585,8 @@ int decode_plan_params(const int32_t* qo_indptr, const int32_t* kv_indptr, const
   if (page_size <= 0) return MI_ERR_INVALID;
   if (page_size % 16) return MI_ERR_UNSUPPORTED;
   if (!supported_head_dim(head_dim)) return MI_ERR_UNSUPPORTED;
-  const SplitLayout L = split_layout(batch, num_kv_heads, head_dim, workspace_bytes - ws_offset);
+  const bool pair = pair_heads(qo_indptr, batch, num_kv_heads, num_qo_heads / num_kv_heads, head_dim);
+  const SplitLayout L = split_layout(batch, num_kv_heads, head_dim, workspace_bytes - ws_offset, pair);
   if (L.max_chunks <= batch || workspace_bytes < ws_offset + L.total) return MI_ERR_WORKSPACE;
   uint8_t* ws = (uint8_t*)workspace + ws_offset;
   PlanParams& pp = *out;
@@ -604,6 +628,16 @@ static void launch_decode(const DecodeParams& dp, int grid, int batch, int phase
   if ((phases & kPhaseMerge) && batch > 0)
     hipLaunchKernelGGL((merge_kernel<MT, D, lane_run(D, FP8 ? 1 : 2)>), dim3((batch * dp.num_kv_heads + 3) / 4),
                        dim3(256), 0, stream, dp, batch);
+}
+
+// Paired kv-heads (dp.num_kv_heads counts pairs): the head_dim 256 kernels.
+template <typename MT, bool FP8>
+static void launch_decode_pair(const DecodeParams& dp, int grid, int batch, int phases, hipStream_t stream) {
+  if (phases & kPhaseAttend)
+    hipLaunchKernelGGL((decode_kernel<MT, FP8, 256, true>), dim3(grid), dim3(256), 0, stream, dp);
+  if ((phases & kPhaseMerge) && batch > 0)
+    hipLaunchKernelGGL((merge_kernel<MT, 256, lane_run(256, FP8 ? 1 : 2), true>),
+                       dim3((batch * dp.num_kv_heads + 3) / 4), dim3(256), 0, stream, dp, batch);
 }
 
 template <int D>
@@ -658,9 +692,15 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
   if (!rows_aligned16(q, q_stride_token, q_stride_head, qesz) ||
       !rows_aligned16(out, out_stride_token, out_stride_head, qesz) || !kv_aligned16(kv))
     return MI_ERR_INVALID;
-  const SplitLayout L = split_layout(batch, nkv, D, workspace_bytes - ws_offset);
+  // the same pairing decision as the plan's (shapes only), so the layouts agree
+  const bool pair = pair_heads(qo_indptr, batch, nkv, num_qo_heads / nkv, D);
+  const SplitLayout L = split_layout(batch, nkv, D, workspace_bytes - ws_offset, pair);
   if (L.max_chunks <= batch || workspace_bytes < ws_offset + L.total) return MI_ERR_WORKSPACE;
   uint8_t* ws = (uint8_t*)workspace + ws_offset;
+  // the paired kernels: 16-bit caches whose pairs' two 128-element rows are
+  // adjacent (NHD pools); fp8, fp32 and other layouts run the per-head
+  // kernels on the same plan
+  const bool pair_kernel = pair && !fp8 && q_dtype != MI_F32 && kv->head_stride == D;
 
   DecodeParams dp{};
   dp.q = q;
@@ -692,6 +732,19 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
   dp.scale_log2 = sm_scale * 1.4426950408889634f;
   const int grid = (int)((L.max_chunks + 7) / 8 * 8 * (int64_t)nkv);
   int st;
+  if (pair_kernel) {
+    dp.num_kv_heads = nkv / 2;
+    dp.head_stride = 2 * kv->head_stride;
+    const int pgrid = (int)((L.max_chunks + 7) / 8 * 8 * (int64_t)(nkv / 2));
+    if (q_dtype == MI_BF16)
+      fp8 ? launch_decode_pair<BF16, true>(dp, pgrid, batch, phases, stream)
+          : launch_decode_pair<BF16, false>(dp, pgrid, batch, phases, stream);
+    else
+      fp8 ? launch_decode_pair<F16, true>(dp, pgrid, batch, phases, stream)
+          : launch_decode_pair<F16, false>(dp, pgrid, batch, phases, stream);
+    MI_CHECK_LAUNCH();
+    return MI_OK;
+  }
   if (q_dtype == MI_F32) {  // fp32 q, cache and output
     st = MI_OK;
     if (phases & kPhaseAttend) st = f32_attend_launch(dp, D, grid, stream);

@@ -12,7 +12,26 @@ struct SplitLayout {
 };
 // ws_avail: bytes the caller's workspace offers from the layout's start (-1:
 // unbounded, giving the recommended size); the chunk budget shrinks to fit.
-SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t ws_avail);
+// pair: the plan is for paired kv-heads (see pair_heads); it only sets the
+// chunk target, the buffers are sized for nkv heads of head_dim either way.
+SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t ws_avail, bool pair = false);
+
+// Decode over head_dim 128 with at most 8 query heads per kv-head reads two
+// adjacent kv-heads as one 256-element row (512 contiguous bytes of a token
+// row instead of 256): each query row takes the 128 elements of its own head
+// and zeros in the other half, so its scores see only its head, and it keeps
+// only its half of the output.  Decided from the call's shapes alone, so a
+// plan and the run that consumes it agree; decode calls only (no qo_indptr),
+// and batches of at least kPairMinBatch requests, whose items are long enough
+// for the one-workgroup-per-CU head_dim 256 kernel (c3, B=256: 542 -> 515 us;
+// c2, B=64, min-chunk items: 57 -> 60 us).  The run uses the paired kernel
+// for 16-bit caches only (fp8 pairs are 256-byte rows: c5 400 -> 410 us).
+constexpr int32_t kPairMinBatch = 128;
+inline bool pair_heads(const int32_t* qo_indptr, int32_t batch, int32_t num_kv_heads, int32_t group,
+                       int32_t head_dim) {
+  return !qo_indptr && batch >= kPairMinBatch && head_dim == 128 && num_kv_heads % 2 == 0 && group >= 1 &&
+         2 * group <= 16;
+}
 
 int decode_plan_impl(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
                      const int32_t* last_page_len, int32_t batch, int32_t page_size,

@@ -168,3 +168,79 @@ def test_decode_long_items_walk_several_page_windows(gpu, hq, hkv, d, ps, fp8):
         f"max_abs={err:.3e}")
     assert hdr[3] > 256 and hdr[2] == len(lens) + 1
     assert err < (TOL_FP8 if fp8 else TOL_BF16)
+
+
+# Decode batches of at least 128 requests at head_dim 128 with at most 8 query
+# heads per kv-head read two adjacent kv-heads as one 256-element row (the
+# query rows of each head in their half, zeros in the other); smaller
+# batches, fp8 and fp32 caches and pools whose heads are not adjacent run the
+# per-head kernels on the same plan.
+PAIR_B = 136
+F32 = torch.float32
+
+
+def _pair_batch(ps, seed, long_lens=(6000, 9001)):
+    """PAIR_B requests: edge lengths, short contexts and long ones the plan splits."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(1, 320, size=PAIR_B)
+    lens[: 4 + len(long_lens)] = [1, 15, 16, 17, *long_lens]
+    pool = int(((lens + ps - 1) // ps).sum()) + 8
+    return (*custom_batch(lens, ps, pool, seed), pool)
+
+
+@pytest.mark.parametrize(
+    "hq,hkv,ps,dtype,fp8",
+    [(32, 4, 16, torch.bfloat16, False), (24, 8, 32, torch.bfloat16, False), (8, 8, 16, torch.float16, False),
+     (28, 4, 48, torch.bfloat16, False), (16, 2, 16, torch.bfloat16, False), (32, 4, 16, torch.bfloat16, True),
+     (32, 4, 16, F32, False)],
+)
+def test_decode_paired_heads(gpu, hq, hkv, ps, dtype, fp8):
+    qo, kv_indptr, kv_indices, last, pool = _pair_batch(ps, seed=hq + ps)
+    out, ref = _run_decode(gpu, hq, hkv, 128, ps, kv_indptr, kv_indices, last, pool, seed=hq, dtype=dtype, fp8=fp8)
+    err = max_abs(out, ref)
+    log(f"decode paired heads hq={hq} hkv={hkv} ps={ps} {dtype} fp8={fp8}: max_abs={err:.3e}")
+    assert err < (TOL_FP8 if fp8 else 2e-5 if dtype == F32 else TOL_BF16)
+
+
+@pytest.mark.parametrize("ps", [16, 32])
+def test_decode_paired_heads_long_items(gpu, ps):
+    """Paired heads with a workspace for batch + 2 items: items of over 256
+    pages, each wavefront walking several 64-page windows, and the longest
+    request split in two (partials + merge of 256-element pair rows)."""
+    qo, kv_indptr, kv_indices, last, pool = _pair_batch(ps, seed=ps, long_lens=(40000, 6000))
+    hdr = []
+    out, ref = _run_decode(gpu, 32, 4, 128, ps, kv_indptr, kv_indices, last, pool, seed=ps + 1,
+                           ws_bytes=_ws_for_items(PAIR_B, 4, 128, PAIR_B + 2), plan_header=hdr)
+    err = max_abs(out, ref)
+    log(f"decode paired long items ps={ps}: items={hdr[2]} item_pages={hdr[3]} max_abs={err:.3e}")
+    assert hdr[3] > 256 and hdr[2] == PAIR_B + 1
+    assert err < TOL_BF16
+
+
+def test_decode_paired_plan_with_padded_heads(gpu):
+    """A pool view whose kv-heads are 160 elements apart (not adjacent) gets
+    the per-head kernel on the paired plan; the padding stays untouched."""
+    hq, hkv, d, ps = 32, 4, 128, 16
+    qo, kv_indptr, kv_indices, last, pool = _pair_batch(ps, seed=21)
+    b = len(last)
+    g = torch.Generator().manual_seed(22)
+    cache_cpu = random_cache(pool, ps, hkv, d, 23)
+    q = torch.randn(b, hq, d, generator=g).to(torch.bfloat16)
+    k_new = torch.randn(b, hkv, d, generator=g).to(torch.bfloat16)
+    v_new = torch.randn(b, hkv, d, generator=g).to(torch.bfloat16)
+    padded = torch.zeros(pool, 2, ps, hkv, 160, dtype=torch.bfloat16, device=gpu)
+    padded[..., :d].copy_(cache_cpu.to(gpu))
+    view = padded[..., :d]
+    loc = P.decode_locations(kv_indptr, kv_indices, last)
+    A.append(cache_cpu, loc[:, 0], loc[:, 1], k_new, v_new, None, None)
+    ref = decode_reference(q, cache_cpu, kv_indptr, kv_indices, last)
+    w = FlashInferDecodeWrapper(workspace(gpu), hq, hkv, d, ps, device=gpu)
+    w.plan(torch.as_tensor(kv_indptr), torch.as_tensor(kv_indices), torch.as_tensor(last))
+    w.set_kv_cache(view, k_new.to(gpu), v_new.to(gpu))
+    out = w.run(q.to(gpu), view)
+    torch.cuda.synchronize()
+    assert torch.equal(view.cpu().view(torch.uint8), cache_cpu.view(torch.uint8)), "append is not bit-exact"
+    assert not padded[..., d:].any().item(), "padding was written"
+    err = max_abs(out, ref)
+    log(f"decode paired plan, padded heads: max_abs={err:.3e}")
+    assert err < TOL_BF16
