@@ -44,6 +44,22 @@
 namespace mi {
 
 constexpr int kMinChunkTokens = 1024;  // never split a request finer than this (4 waves x 256)
+// ... except in small jobs, down to this, while the items fit one round of
+// resident workgroups (decode_plan_body)
+constexpr int kSmallChunkTokens = 256;
+
+// Compute units of the current device (cached per device).
+static int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
 
 
 // Target number of wavefronts for one plan: ~4K (item, kv-head, quarter)
@@ -599,6 +615,13 @@ int decode_plan_params(const int32_t* qo_indptr, const int32_t* kv_indptr, const
   pp.target = L.max_chunks - batch;
   pp.min_chunk_pages = (kMinChunkTokens + page_size - 1) / page_size;
   pp.max_chunks = L.max_chunks;
+  // resident workgroups per kv-head (or pair): two per CU at head_dim <= 128,
+  // one for the head_dim 256 kernels
+  const int heads = pair ? num_kv_heads / 2 : num_kv_heads;
+  const int per_cu = (pair || head_dim > 128) ? 1 : 2;
+  const int slots = device_cu_count() * per_cu / heads;
+  pp.slots = slots < 1 ? 1 : (slots < L.max_chunks ? slots : L.max_chunks);
+  pp.floor_pages = (kSmallChunkTokens + page_size - 1) / page_size;
   pp.group = num_qo_heads / num_kv_heads;
   pp.hdr = (int32_t*)(ws + L.hdr);
   pp.chunk_indptr = (int32_t*)(ws + L.chunk_indptr);

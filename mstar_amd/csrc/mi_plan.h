@@ -36,6 +36,7 @@ struct PlanParams {
   const int32_t* kv_indices;
   const int32_t* last_page_len;
   int32_t batch, target, min_chunk_pages, max_chunks, group;
+  int32_t slots, floor_pages;  // small jobs: items of down to floor_pages while at most `slots` items
   int32_t* hdr;
   int32_t* chunk_indptr;
   int4* work;
@@ -50,11 +51,15 @@ struct PlanParams {
 // (request, index within the request, end page, items of the request); its
 // partial lives at chunk_indptr[request] + index whatever its list position.
 constexpr int kSizeBuckets = 64;
+// Small jobs cut a request into at most this many items: its partials are
+// merged by one wavefront, one or two at a time.
+constexpr int kMaxSmallItems = 8;
 
 // One 1024-thread workgroup builds the plan.
 __device__ inline void decode_plan_body(const PlanParams& p) {
   __shared__ int smem[16];
   __shared__ int s_bucket[kSizeBuckets];
+  __shared__ int s_max_pages;
   int total_pages = 0;
   if (p.num_pages) {
     for (int base = 0; base < p.batch; base += 1024) {
@@ -66,17 +71,56 @@ __device__ inline void decode_plan_body(const PlanParams& p) {
   } else {
     total_pages = p.kv_indptr[p.batch] - p.kv_indptr[0];
   }
-  int cp = (total_pages + p.target - 1) / p.target;
-  if (cp < p.min_chunk_pages) cp = p.min_chunk_pages;
-  if (threadIdx.x < kSizeBuckets) s_bucket[threadIdx.x] = 0;
-  __syncthreads();
-  auto items_of = [&](int b, int& np, int& n, int& full, int& rem_bucket) {
+  // items of request b at `c` pages per item (0 for requests this kernel does not serve)
+  auto count_of = [&](int b, int c, int& np) {
     np = p.num_pages ? p.num_pages[b] : p.kv_indptr[b + 1] - p.kv_indptr[b];
-    n = np > 0 ? (np + cp - 1) / cp : 0;
+    int n = np > 0 ? (np + c - 1) / c : 0;
     if (p.qo_indptr) {  // ragged batch: only short-query requests belong to this kernel
       const int qo_len = p.qo_indptr[b + 1] - p.qo_indptr[b];
       if (qo_len <= 0 || qo_len * p.group > kRows) n = 0;
     }
+    return n;
+  };
+  int cp = (total_pages + p.target - 1) / p.target;
+  if (cp < p.min_chunk_pages) {
+    // A small job: the shortest items, down to floor_pages, whose count still
+    // fits one round of resident workgroups, so a handful of requests is not
+    // streamed by a handful of workgroups (a one-request decode over 1k
+    // tokens would otherwise be one workgroup's work), and no more than
+    // kMaxSmallItems items for the longest request.
+    if (threadIdx.x == 0) s_max_pages = 0;
+    __syncthreads();
+    for (int b = (int)threadIdx.x; b < p.batch; b += 1024) {  // the longest request served
+      int np = 0;
+      if (count_of(b, 1, np) > 0) atomicMax(&s_max_pages, np);
+    }
+    __syncthreads();
+    int hi = p.min_chunk_pages;
+    int lo = p.floor_pages;
+    if (lo < cp) lo = cp;
+    if (lo < (s_max_pages + kMaxSmallItems - 1) / kMaxSmallItems) lo = (s_max_pages + kMaxSmallItems - 1) / kMaxSmallItems;
+    if (lo > hi) lo = hi;
+    if (lo < 1) lo = 1;
+    while (lo < hi) {  // uniform across the workgroup: every thread sees the same totals
+      const int mid = (lo + hi) >> 1;
+      int cnt = 0;
+      for (int base = 0; base < p.batch; base += 1024) {
+        const int b = base + (int)threadIdx.x;
+        int np = 0;
+        const int n = b < p.batch ? count_of(b, mid, np) : 0;
+        int tot;
+        block_exclusive_scan_1024(n, tot, smem);
+        cnt += tot;
+      }
+      if (cnt <= p.slots) hi = mid;
+      else lo = mid + 1;
+    }
+    cp = lo;
+  }
+  if (threadIdx.x < kSizeBuckets) s_bucket[threadIdx.x] = 0;
+  __syncthreads();
+  auto items_of = [&](int b, int& np, int& n, int& full, int& rem_bucket) {
+    n = count_of(b, cp, np);
     full = n > 0 ? np / cp : 0;
     const int rem = n > 0 ? np - full * cp : 0;
     rem_bucket = rem > 0 ? (int)(((int64_t)rem * kSizeBuckets - 1) / cp) : -1;

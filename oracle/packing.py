@@ -137,20 +137,42 @@ def decode_locations(kv_indptr, kv_indices, last_page_len) -> np.ndarray:
 
 
 def split_chunks(kv_indptr, page_size: int, target_units: int, num_kv_heads: int,
-                 min_chunk_tokens: int = 1024) -> tuple[int, np.ndarray]:
+                 min_chunk_tokens: int = 1024, slots: int | None = None, small_chunk_tokens: int = 256,
+                 max_small_items: int = 8) -> tuple[int, np.ndarray]:
     """Split-KV partition rule of the GPU plan: (item_pages, items per request).
 
-    item_pages = max(ceil(min_chunk_tokens/page_size), ceil(total_pages/target)),
     target = max(16, target_units // (4 * num_kv_heads)) (4 wavefronts per
-    item); each request's page list is cut into ceil(pages/item_pages)
-    consecutive items.  This is the build's own schedule (FlashInfer's is not
-    reproduced); the attention result must not depend on it beyond rounding.
+    item) and item_pages = max(ceil(min_chunk_tokens/page_size),
+    ceil(total_pages/target)), except for a small job (ceil(total_pages/target)
+    below the minimum chunk) when ``slots`` is given: then item_pages is the
+    smallest value in [lo, ceil(min_chunk_tokens/page_size)] whose item count
+    is at most ``slots``, with lo = max(ceil(small_chunk_tokens/page_size),
+    ceil(total_pages/target), ceil(longest request's pages/max_small_items)).
+    Each request's page list is cut into ceil(pages/item_pages) consecutive
+    items.  This is the build's own schedule (FlashInfer's is not reproduced);
+    the attention result must not depend on it beyond rounding.
     """
     kv_indptr = np.asarray(kv_indptr, dtype=np.int64)
     npages = np.diff(kv_indptr)
     target = max(16, target_units // (4 * num_kv_heads))
     total = int(kv_indptr[-1] - kv_indptr[0])
-    cp = max(-(-min_chunk_tokens // page_size), -(-total // target))
+    cmin = -(-min_chunk_tokens // page_size)
+    cp = -(-total // target)
+    count = lambda c: int(np.where(npages > 0, -(-npages // c), 0).sum())
+    if cp >= cmin or slots is None:
+        cp = max(cp, cmin)
+    else:
+        longest = int(npages.max(initial=0))
+        lo = max(-(-small_chunk_tokens // page_size), cp, -(-longest // max_small_items), 1)
+        lo = min(lo, cmin)
+        hi = cmin
+        while lo < hi:
+            mid = (lo + hi) // 2
+            if count(mid) <= slots:
+                hi = mid
+            else:
+                lo = mid + 1
+        cp = lo
     return cp, np.where(npages > 0, -(-npages // cp), 0)
 
 

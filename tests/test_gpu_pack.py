@@ -112,7 +112,9 @@ def test_decode_plan_partition(gpu):
     torch.cuda.synchronize()
     hdr, ci, wk, max_chunks = _split_layout(len(lens), hkv, d)
     h = ws[hdr:hdr + 20].cpu().view(torch.int32).tolist()
-    cp, nchunks = P.split_chunks(kv_indptr, 16, 4096, hkv)
+    # a small job is cut for the CUs: two items per CU per kv-head at head_dim 128
+    slots = min(torch.cuda.get_device_properties(0).multi_processor_count * 2 // hkv, max_chunks)
+    cp, nchunks = P.split_chunks(kv_indptr, 16, 4096, hkv, slots=slots)
     assert h[0] == 0x4D494450 and h[1] == len(lens) and h[3] == cp and h[2] == int(nchunks.sum())
     cptr = ws[ci:ci + 4 * (len(lens) + 1)].cpu().view(torch.int32).numpy()
     assert cptr.tolist() == [0] + np.cumsum(nchunks).tolist()

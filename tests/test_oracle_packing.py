@@ -173,6 +173,29 @@ def test_split_chunks_cover_every_page_once():
             assert (k - 1) * cp < npg <= k * cp
 
 
+def test_split_chunks_small_job_rule_against_brute_force():
+    # a small job: the smallest item size in [lo, min chunk] whose item count fits the slots
+    rng = np.random.default_rng(5)
+    for trial in range(200):
+        n = int(rng.integers(1, 12))
+        pages = rng.integers(0, 300, n)
+        kv_indptr = np.concatenate([[0], np.cumsum(pages)])
+        slots = int(rng.integers(1, 200))
+        cp, k = P.split_chunks(kv_indptr, 16, 4096, 4, slots=slots)
+        total, cmin = int(pages.sum()), 64
+        cnt = lambda c: sum(-(-int(x) // c) for x in pages)
+        ctarget = -(-total // 256)
+        if ctarget >= cmin:
+            assert cp == ctarget
+            continue
+        lo = min(max(16, ctarget, -(-int(pages.max()) // 8), 1), cmin)
+        fits = [c for c in range(lo, cmin + 1) if cnt(c) <= slots]
+        assert cp == (fits[0] if fits else cmin), (trial, pages.tolist(), slots, cp)
+        assert int(k.sum()) == cnt(cp) and all(-(-int(x) // cp) <= 8 or cp == cmin for x in pages)
+    # without slots the rule is the plain minimum chunk
+    assert P.split_chunks(np.array([0, 5, 9]), 16, 4096, 4)[0] == 64
+
+
 def test_snapshot_copies_history_and_keeps_leading_pages():
     import torch
 
