@@ -467,18 +467,18 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 }
 
 // ----------------------------------------------------------------- merge
-// One wavefront per (request, kv-head); lane l merges what lane l of the
-// decode wavefronts held: row l%16, output elements
-// d = VW*(4*(l/16) + r) + j, read from the register-order partial layout with
-// 64-lane contiguous (cache-line) loads.  Four wavefronts per workgroup.
+// One workgroup per (request, kv-head); its 4 wavefronts split the output
+// elements as the decode kernel's did: lane l of wavefront w merges row l%16,
+// elements d = VW*(4*(l/16) + w) + j, read from the register-order partial
+// layout with 64-lane contiguous (cache-line) loads.
 template <typename MT, int D, int RUN, bool PAIR = false>
 __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batch) {
   static_assert(!PAIR || D == 256, "paired kv-heads form 256-element rows");
   constexpr int VW = D / 16;
-  constexpr int NS = 4 * VW / 4;  // float4 stores per lane per partial
+  constexpr int NS = VW / 4;  // float4 groups per lane per partial
   constexpr float kNegInf = -__builtin_inff();
   const int nkv = p.num_kv_heads;
-  const int pair = (int)blockIdx.x * 4 + ((int)threadIdx.x >> 6);
+  const int pair = (int)blockIdx.x;
   if (pair >= batch * nkv) return;
   const int b = pair / nkv;
   const int h = pair - b * nkv;
@@ -494,6 +494,7 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
   const int rows = (PAIR ? 2 : 1) * qo_len * G;
   if (rows > kRows) return;  // long-query request: written by the prefill kernel
   const int lane = lane_id();
+  const int wave = (int)threadIdx.x >> 6;
   const int col = lane & 15, grp = lane >> 4;
   if (col >= rows) return;
   const int half = PAIR && col >= qo_len * G ? 1 : 0;
@@ -508,7 +509,7 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
   // once (no separate max pass ahead of the loads), and the running sum is
   // rescaled when a partial raises the running max.
   float M = kNegInf, wsum = 0.f;
-  constexpr int U = D > 128 ? 2 : 4;  // partials in flight per step
+  constexpr int U = D > 128 ? 4 : 8;  // partials in flight per step
   for (int c = 0; c < nb; c += U) {
     float w[U];
     float4 o[U][NS];
@@ -518,7 +519,7 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
       if (c + u < nb) {
         const int64_t unit = u0 + (int64_t)(c + u) * nkv;
         w[u] = p.lse_part[unit * kRows + col];
-        const float* src = p.o_part + unit * kRows * D + 4 * lane;
+        const float* src = p.o_part + unit * kRows * D + 4 * lane + 256 * wave * NS;
 #pragma unroll
         for (int i = 0; i < NS; ++i) o[u][i] = *(const float4*)(src + 256 * i);
       }
@@ -551,36 +552,30 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
   const int64_t orow_off = (int64_t)(qo_start + qtok) * p.out_stride_tok + (int64_t)(hq * G + g) * p.out_stride_head;
-  // store i = r*(VW/4) + j/4 holds d = VW*(4*grp + r) + j .. +3
+  // this wave's elements of the row: group i holds d = dim_of(RUN, 4*grp + wave, 4*i) .. +3
   if constexpr (MT::kDtype == MI_F32) {
     float* orow = (float*)p.out + orow_off;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int jj = 0; jj < VW / 4; ++jj) {
-        const float4 a = acc[r * (VW / 4) + jj];
-        *(float4*)(orow + dim_of(RUN, 4 * grp + r, 4 * jj)) = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
-      }
+    for (int i = 0; i < NS; ++i) {
+      const float4 a = acc[i];
+      *(float4*)(orow + dim_of(RUN, 4 * grp + wave, 4 * i)) = make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+    }
   } else {
     uint16_t* orow = (uint16_t*)p.out + orow_off;
+    uint32_t w[VW / 2];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      uint32_t w[VW / 2];
+    for (int i = 0; i < NS; ++i) {
+      w[2 * i] = MT::pack2(acc[i].x * inv, acc[i].y * inv);
+      w[2 * i + 1] = MT::pack2(acc[i].z * inv, acc[i].w * inv);
+    }
+    if constexpr (VW == 4) {
+      *(uint2*)(orow + dim_of(RUN, 4 * grp + wave, 0)) = make_uint2(w[0], w[1]);
+    } else {
 #pragma unroll
-      for (int jj = 0; jj < VW / 4; ++jj) {
-        const float4 a = acc[r * (VW / 4) + jj];
-        w[2 * jj] = MT::pack2(a.x * inv, a.y * inv);
-        w[2 * jj + 1] = MT::pack2(a.z * inv, a.w * inv);
-      }
-      if constexpr (VW == 4) {
-        *(uint2*)(orow + dim_of(RUN, 4 * grp + r, 0)) = make_uint2(w[0], w[1]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VW / 2; i += 4) {
-          const int d0 = dim_of(RUN, 4 * grp + r, 2 * i);  // 8 consecutive elements
-          if (PAIR && (d0 >= D / 2) != (half == 1)) continue;  // the other head's half
-          *(uint4*)(orow + d0 - (PAIR ? (D / 2) * half : 0)) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
-        }
+      for (int i = 0; i < VW / 2; i += 4) {
+        const int d0 = dim_of(RUN, 4 * grp + wave, 2 * i);  // 8 consecutive elements
+        if (PAIR && (d0 >= D / 2) != (half == 1)) continue;  // the other head's half
+        *(uint4*)(orow + d0 - (PAIR ? (D / 2) * half : 0)) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
       }
     }
   }
@@ -649,7 +644,7 @@ static void launch_decode(const DecodeParams& dp, int grid, int batch, int phase
   if (phases & kPhaseAttend)
     hipLaunchKernelGGL((decode_kernel<MT, FP8, D>), dim3(grid), dim3(256), 0, stream, dp);
   if ((phases & kPhaseMerge) && batch > 0)
-    hipLaunchKernelGGL((merge_kernel<MT, D, lane_run(D, FP8 ? 1 : 2)>), dim3((batch * dp.num_kv_heads + 3) / 4),
+    hipLaunchKernelGGL((merge_kernel<MT, D, lane_run(D, FP8 ? 1 : 2)>), dim3(batch * dp.num_kv_heads),
                        dim3(256), 0, stream, dp, batch);
 }
 
@@ -660,12 +655,12 @@ static void launch_decode_pair(const DecodeParams& dp, int grid, int batch, int 
     hipLaunchKernelGGL((decode_kernel<MT, FP8, 256, true>), dim3(grid), dim3(256), 0, stream, dp);
   if ((phases & kPhaseMerge) && batch > 0)
     hipLaunchKernelGGL((merge_kernel<MT, 256, lane_run(256, FP8 ? 1 : 2), true>),
-                       dim3((batch * dp.num_kv_heads + 3) / 4), dim3(256), 0, stream, dp, batch);
+                       dim3(batch * dp.num_kv_heads), dim3(256), 0, stream, dp, batch);
 }
 
 template <int D>
 static void launch_merge_f32(const DecodeParams& dp, int batch, hipStream_t stream) {
-  hipLaunchKernelGGL((merge_kernel<F32Out, D, lane_run(D, 4)>), dim3((batch * dp.num_kv_heads + 3) / 4), dim3(256),
+  hipLaunchKernelGGL((merge_kernel<F32Out, D, lane_run(D, 4)>), dim3(batch * dp.num_kv_heads), dim3(256),
                      0, stream, dp, batch);
 }
 
