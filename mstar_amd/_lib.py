@@ -222,6 +222,35 @@ def memcpy_h2d_async(dst: int, src: int, nbytes: int, stream: int) -> None:
         raise RuntimeError(f"hipMemcpyAsync failed with HIP error {rc}")
 
 
+_event_fns = None
+
+
+def _events_api():
+    """hipEventCreateWithFlags / hipEventRecord / hipEventSynchronize of the
+    HIP runtime this library is bound to."""
+    global _event_fns
+    if _event_fns is None:
+        h = lib()
+        create, record, sync = h.hipEventCreateWithFlags, h.hipEventRecord, h.hipEventSynchronize
+        create.restype = record.restype = sync.restype = ctypes.c_int
+        create.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        record.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        sync.argtypes = [ctypes.c_void_p]
+        _event_fns = (create, record, sync)
+    return _event_fns
+
+
+def _event_create(device: torch.device) -> int:
+    """A timing-free HIP event on ``device`` (kept for the life of the process)."""
+    create = _events_api()[0]
+    ev = ctypes.c_void_p()
+    with torch.cuda.device(device):
+        rc = create(ctypes.byref(ev), 2)  # 2 = hipEventDisableTiming
+    if rc != 0:
+        raise RuntimeError(f"hipEventCreateWithFlags failed with HIP error {rc}")
+    return ev.value
+
+
 class PinnedUploader:
     """Small int32 host arrays to the device through two pinned staging buffers.
 
@@ -247,21 +276,26 @@ class PinnedUploader:
             i = self._i
             self._i ^= 1
             ev = self._events[i]
+            _, record, sync = _events_api()
             if ev is not None:
-                ev.synchronize()  # the copy that last read this buffer is done
+                rc = sync(ev)  # the copy that last read this buffer is done
+                if rc != 0:
+                    raise RuntimeError(f"hipEventSynchronize failed with HIP error {rc}")
             buf = self._bufs[i]
             if buf is None or buf[1].size < n:
                 t = torch.empty(max(n, 4096), dtype=torch.int32, pin_memory=True)
-                buf = self._bufs[i] = (t, t.numpy())
+                buf = self._bufs[i] = (t, t.numpy(), t.data_ptr())
             buf[1][:n] = arr
             dev = torch.empty(max(n, 1), dtype=torch.int32, device=self.device)
             stream = stream_ptr(self.device)
             if n:
-                memcpy_h2d_async(dev.data_ptr(), buf[0].data_ptr(), 4 * n, stream)
+                memcpy_h2d_async(dev.data_ptr(), buf[2], 4 * n, stream)
             if ev is None:
-                ev = self._events[i] = torch.cuda.Event()
-            ev.record(torch.cuda.current_stream(self.device))
-        return dev[:n]
+                ev = self._events[i] = _event_create(self.device)
+            rc = record(ev, stream)
+            if rc != 0:
+                raise RuntimeError(f"hipEventRecord failed with HIP error {rc}")
+        return dev if n == dev.shape[0] else dev[:n]
 
 
 _uploaders: dict = {}

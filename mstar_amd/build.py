@@ -66,8 +66,31 @@ def _compile(src: Path, hipcc: str) -> Path:
     return obj
 
 
+def build_host(verbose: bool = True) -> Path:
+    """Compile ``csrc/host_step.c`` (the planning step's host bookkeeping) into
+    the CPython extension ``mstar_amd/_host_step``."""
+    import sysconfig
+
+    cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        raise RuntimeError("no C compiler for the host_step extension")
+    out = PKG_DIR / ("_host_step" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_suffix(".tmp")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}", str(CSRC / "host_step.c"),
+           "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"host_step build failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}", file=sys.stderr)
+    return out
+
+
 def build(verbose: bool = True) -> Path:
-    """Compile all HIP sources for gfx950 and link ``libmstar_amd.so``."""
+    """Compile all HIP sources for gfx950 and link ``libmstar_amd.so``; build
+    the host_step extension."""
+    build_host(verbose)
     hipcc = _hipcc()
     BUILD_DIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))

@@ -29,7 +29,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .kv_store import KVCacheConfig, KVRequestState, PagedAllocationManager
+from .kv_store import KVCacheConfig, KVRequestState, PagedAllocationManager, _host_step
 from .paged_attention import PagedDecodeWrapper, PagedPrefillWrapper
 from .rope import apply_llama31_rope_pos_ids_inplace, apply_rope_pos_ids_inplace, rope_positions
 from .trace import trace_range
@@ -174,6 +174,9 @@ class BatchedCacheManager:
         if states is None:
             generation = self.alloc_manager.state_generation
             states = [self._get_state(rid, label) for rid, label in entries]
+        am = self.alloc_manager
+        if _host_step is not None and am.block_table is not None:
+            return am.alloc_pack_meta(entries, states, seq_lens, generation)
         seq = np.array([st.seq_len for st in states], dtype=np.int64)
         sl = np.asarray(seq_lens, dtype=np.int64).reshape(n)
         self.alloc_manager.alloc_batch(entries, states, seq + sl, generation)
@@ -201,12 +204,14 @@ class BatchedCacheManager:
         self._states_cache[label] = (gen, key, entries, states)
         return entries, states, gen
 
-    def _launch_pack(self, meta: np.ndarray, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=None) -> None:
+    def _launch_pack(self, meta: np.ndarray, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=None,
+                     total_pages: int | None = None) -> None:
         """One upload of the step's metadata + new pages, one pack kernel; with
         ``plan_wrapper`` (a decode wrapper, decode step) the same launch also
         writes that wrapper's split-KV plan (``mi_pack_plan``)."""
         b = qo.shape[0] - 1
-        total_pages = int(meta[3 * b:4 * b].sum())
+        if total_pages is None:
+            total_pages = int(meta[3 * b:4 * b].sum())
         dmeta = self._pack.upload(meta)
         bt = self.alloc_manager.block_table
         grid = max(1, min(256, (total_pages + 1023) // 1024))  # about one page per thread
@@ -277,7 +282,8 @@ class BatchedCacheManager:
         fused = isinstance(wrapper, PagedDecodeWrapper) and is_decode and (not graph_static or b == wrapper.batch_size)
         # device side: one upload of the step's metadata and one pack launch (the reference's torch.tensor builds)
         with trace_range(nv, "cache.plan_attention.make_tensors"):
-            self._launch_pack(meta, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=wrapper if fused else None)
+            self._launch_pack(meta, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=wrapper if fused else None,
+                              total_pages=total_pages)
         self._last_pack = (qo, kv_indptr, kv_indices[:total_pages], last, loc)
         with trace_range(nv, "cache.plan_attention.wrapper_plan"):
             if fused:
@@ -564,10 +570,13 @@ class BatchedCacheManager:
             label = labels.pop()
             ps = self._plan_states[label]
             _, states, _ = self._label_states(label)
-            adv = ps.custom_pos_advance if ps.custom_pos_advance is not None else ps.seq_lens
-            for st, n, a in zip(states, ps.seq_lens, adv):
-                st.seq_len += n
-                st.position_id_start += a
+            if _host_step is not None:
+                _host_step.advance(states, ps.seq_lens, ps.custom_pos_advance)
+            else:
+                adv = ps.custom_pos_advance if ps.custom_pos_advance is not None else ps.seq_lens
+                for st, n, a in zip(states, ps.seq_lens, adv):
+                    st.seq_len += n
+                    st.position_id_start += a
             for ps in self._plan_states.values():
                 ps.custom_pos_advance = None
             return

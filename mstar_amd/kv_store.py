@@ -36,6 +36,11 @@ import torch
 
 from . import _lib
 
+try:  # the planning step's per-request loops in C (csrc/host_step.c); the Python loops below specify them
+    from . import _host_step
+except ImportError:  # not built yet
+    _host_step = None
+
 
 class PageAllocator:
     """Thread-safe FIFO page allocator (``kv_store.py:25-67``)."""
@@ -387,6 +392,33 @@ class PagedAllocationManager:
                         ),
                     )
                 state.page_indices.extend(new_pages)
+
+    def alloc_pack_meta(self, entries: list[tuple[str, str]], states: list[KVRequestState], seq_lens,
+                        generation: int | None = None) -> np.ndarray:
+        """:meth:`alloc_batch` to ``seq_len + seq_lens[i]`` followed by the block
+        table's :meth:`DeviceBlockTable.prepare_meta`, in the host_step extension:
+        the pack kernel's int32 input ``[slot | seq_len | new_len | num_pages |
+        pages on the device]`` (one entry per state each) followed by the pages
+        not yet on the device.  Same allocation order, errors and state
+        updates as the two Python methods."""
+        hs = _host_step
+        bt = self.block_table
+        sl = list(seq_lens)
+        with self._lock:
+            if generation is None or generation != self.state_generation:
+                for i, (rid, label) in enumerate(entries):
+                    live = self.get_state(rid, label)
+                    if live is not states[i]:
+                        states[i] = live
+            total, need = hs.needs(states, sl, self.config.page_size)
+            pages = None
+            if total:
+                pages = self.page_allocator.try_allocate(total)
+                if pages is None:  # entry by entry: the first that does not fit raises, earlier ones keep theirs
+                    for i in np.flatnonzero(np.frombuffer(need, dtype=np.int32) > 0).tolist():
+                        self.alloc(entries[i][0], entries[i][1], states[i].seq_len + int(sl[i]))
+            meta = hs.extend_meta(states, sl, need, pages, bt.stride, bt.acquire)
+        return np.frombuffer(meta, dtype=np.int32)
 
     def alloc_batch(self, entries: list[tuple[str, str]], states: list[KVRequestState],
                     seq_lens_after: np.ndarray, generation: int | None = None) -> None:

@@ -318,7 +318,8 @@ class PagedDecodeWrapper(_FusedRopeAppend):
         """Paged decode attention (``flashinfer_utils.py:455-465``): q ``[n_req, Hq, D]`` -> o."""
         if self.dtype is None:
             raise RuntimeError("plan() must be called before run()")
-        q = q.to(self.dtype)
+        if q.dtype != self.dtype:
+            q = q.to(self.dtype)
         n = self._n_req
         if q.dim() != 3 or q.shape[0] < n or q.shape[1] != self.num_qo_heads or q.shape[2] != self.head_dim:
             raise ValueError(f"q shape {tuple(q.shape)} does not match the plan")
@@ -501,7 +502,8 @@ class PagedPrefillWrapper(_FusedRopeAppend):
         """Ragged paged attention (``flashinfer_utils.py:258-269``): q ``[tokens, Hq, D]`` -> o."""
         if self.dtype is None:
             raise RuntimeError("plan() must be called before run()")
-        q = q.to(self.dtype)
+        if q.dtype != self.dtype:
+            q = q.to(self.dtype)
         if q.dim() != 3 or q.shape[1] != self.num_qo_heads or q.shape[2] != self.head_dim:
             raise ValueError(f"q shape {tuple(q.shape)} does not match the wrapper")
         if q.stride(2) != 1 or q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:

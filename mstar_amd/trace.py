@@ -15,9 +15,6 @@ Ranges are host-side markers only: no device synchronisation.
 
 from __future__ import annotations
 
-from contextlib import contextmanager
-from typing import Iterator
-
 import torch
 
 
@@ -29,14 +26,38 @@ def range_pop() -> None:
     torch.cuda.nvtx.range_pop()
 
 
-@contextmanager
-def trace_range(enabled: bool, name: str) -> Iterator[None]:
-    """``range_push(name)`` ... ``range_pop()`` around the block when ``enabled``."""
-    if not enabled:
-        yield
-        return
-    range_push(name)
-    try:
-        yield
-    finally:
+class _Range:
+    """``range_push(name)`` on entry, ``range_pop()`` on exit."""
+
+    __slots__ = ("name",)
+
+    def __init__(self, name: str):
+        self.name = name
+
+    def __enter__(self) -> None:
+        range_push(self.name)
+
+    def __exit__(self, *exc) -> bool:
         range_pop()
+        return False
+
+
+class _NoRange:
+    """The disabled range: nothing on entry or exit (one shared instance, so a
+    disabled range costs a call and two no-op methods per phase)."""
+
+    __slots__ = ()
+
+    def __enter__(self) -> None:
+        return None
+
+    def __exit__(self, *exc) -> bool:
+        return False
+
+
+_NO_RANGE = _NoRange()
+
+
+def trace_range(enabled: bool, name: str):
+    """Context manager: ``range_push(name)`` ... ``range_pop()`` around the block when ``enabled``."""
+    return _Range(name) if enabled else _NO_RANGE
