@@ -129,4 +129,32 @@ __device__ __forceinline__ int block_exclusive_scan_1024(int v, int& total, int*
   return before + x - v;
 }
 
+// Sum and max of v over a 1024-thread workgroup, returned to every thread
+// (smem: 16 ints, free again on return).
+__device__ __forceinline__ int block_sum_1024(int v, int* smem) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if (lane == 0) smem[w] = v;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) t += smem[i];
+  __syncthreads();
+  return t;
+}
+
+__device__ __forceinline__ int block_max_1024(int v, int* smem) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  if (lane == 0) smem[w] = v;
+  __syncthreads();
+  int t = smem[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) t = max(t, smem[i]);
+  __syncthreads();
+  return t;
+}
+
 }  // namespace mi

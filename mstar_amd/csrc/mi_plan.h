@@ -59,7 +59,6 @@ constexpr int kMaxSmallItems = 8;
 __device__ inline void decode_plan_body(const PlanParams& p) {
   __shared__ int smem[16];
   __shared__ int s_bucket[kSizeBuckets];
-  __shared__ int s_max_pages;
   int total_pages = 0;
   if (p.num_pages) {
     for (int base = 0; base < p.batch; base += 1024) {
@@ -88,34 +87,54 @@ __device__ inline void decode_plan_body(const PlanParams& p) {
     // streamed by a handful of workgroups (a one-request decode over 1k
     // tokens would otherwise be one workgroup's work), and no more than
     // kMaxSmallItems items for the longest request.
-    if (threadIdx.x == 0) s_max_pages = 0;
-    __syncthreads();
-    for (int b = (int)threadIdx.x; b < p.batch; b += 1024) {  // the longest request served
+    // Page counts are read once (batch <= 1024: one request per thread).
+    const bool one = p.batch <= 1024;
+    int mine = 0;  // pages of this thread's request if this kernel serves it
+    if (one && (int)threadIdx.x < p.batch) {
       int np = 0;
-      if (count_of(b, 1, np) > 0) atomicMax(&s_max_pages, np);
+      if (count_of((int)threadIdx.x, 1, np) > 0) mine = np;
     }
-    __syncthreads();
-    int hi = p.min_chunk_pages;
-    int lo = p.floor_pages;
-    if (lo < cp) lo = cp;
-    if (lo < (s_max_pages + kMaxSmallItems - 1) / kMaxSmallItems) lo = (s_max_pages + kMaxSmallItems - 1) / kMaxSmallItems;
-    if (lo > hi) lo = hi;
-    if (lo < 1) lo = 1;
-    while (lo < hi) {  // uniform across the workgroup: every thread sees the same totals
-      const int mid = (lo + hi) >> 1;
+    auto items_at = [&](int c) {  // the workgroup's item count at c pages per item
+      if (one) return block_sum_1024(mine > 0 ? (mine + c - 1) / c : 0, smem);
       int cnt = 0;
       for (int base = 0; base < p.batch; base += 1024) {
         const int b = base + (int)threadIdx.x;
         int np = 0;
-        const int n = b < p.batch ? count_of(b, mid, np) : 0;
-        int tot;
-        block_exclusive_scan_1024(n, tot, smem);
-        cnt += tot;
+        cnt += block_sum_1024(b < p.batch ? count_of(b, c, np) : 0, smem);
       }
-      if (cnt <= p.slots) hi = mid;
-      else lo = mid + 1;
+      return cnt;
+    };
+    int longest = 0;
+    if (one) {
+      longest = block_max_1024(mine, smem);
+    } else {
+      int m = 0;
+      for (int b = (int)threadIdx.x; b < p.batch; b += 1024) {
+        int np = 0;
+        if (count_of(b, 1, np) > 0) m = max(m, np);
+      }
+      longest = block_max_1024(m, smem);
     }
-    cp = lo;
+    const int hi = p.min_chunk_pages;
+    int lo = p.floor_pages;
+    if (lo < cp) lo = cp;
+    if (lo < (longest + kMaxSmallItems - 1) / kMaxSmallItems) lo = (longest + kMaxSmallItems - 1) / kMaxSmallItems;
+    if (lo > hi) lo = hi;
+    if (lo < 1) lo = 1;
+    // The smallest size in [lo, hi] whose items fit the slots (counts fall as
+    // the size grows), or hi when none does.  Uniform across the workgroup:
+    // every thread sees the same totals.
+    if (lo < hi && items_at(hi) <= p.slots) {
+      int h = hi;
+      while (lo < h) {
+        const int mid = (lo + h) >> 1;
+        if (items_at(mid) <= p.slots) h = mid;
+        else lo = mid + 1;
+      }
+      cp = lo;
+    } else {
+      cp = lo < hi ? hi : lo;
+    }
   }
   if (threadIdx.x < kSizeBuckets) s_bucket[threadIdx.x] = 0;
   __syncthreads();

@@ -97,12 +97,20 @@ def _split_layout(batch, nkv, d, units=4096):
     return hdr, chunk_indptr, work, max_chunks
 
 
-def test_decode_plan_partition(gpu):
+@pytest.mark.parametrize("lens,pool,hq,hkv", [
+    ([0, 1, 16, 17, 300, 5000, 32768, 4096, 77], 4000, 32, 4),
+    # a small job whose item size falls strictly inside the search range (21 pages on 256 CUs)
+    ([2000] * 20 + [0, 5], 3000, 32, 4),
+    # a small job whose items cannot fit the slots at any size: the minimum chunk
+    # (below the batch size that pairs kv-heads, which this plan model leaves out)
+    ([1000] * 100, 7000, 24, 8),
+])
+def test_decode_plan_partition(gpu, lens, pool, hq, hkv):
     from gpu_helpers import custom_batch
 
-    lens = [0, 1, 16, 17, 300, 5000, 32768, 4096, 77]
-    qo, kv_indptr, kv_indices, last = custom_batch(lens, 16, 4000, seed=2)
-    hq, hkv, d = 32, 4, 128
+    log(f"decode plan partition: {len(lens)} requests, {sum(lens)} tokens")
+    qo, kv_indptr, kv_indices, last = custom_batch(lens, 16, pool, seed=2)
+    d = 128
     ws = workspace(gpu, 256 << 20)
     loc = torch.full((len(lens), 2), -7, dtype=torch.long, device=gpu)
     ti = lambda x: torch.as_tensor(x).to(gpu)
@@ -113,8 +121,10 @@ def test_decode_plan_partition(gpu):
     hdr, ci, wk, max_chunks = _split_layout(len(lens), hkv, d)
     h = ws[hdr:hdr + 20].cpu().view(torch.int32).tolist()
     # a small job is cut for the CUs: two items per CU per kv-head at head_dim 128
+    assert len(lens) < 128, "a paired-head plan has another split target"
     slots = min(torch.cuda.get_device_properties(0).multi_processor_count * 2 // hkv, max_chunks)
     cp, nchunks = P.split_chunks(kv_indptr, 16, 4096, hkv, slots=slots)
+    log(f"  slots={slots} item pages: plan {h[3]}, oracle {cp}")
     assert h[0] == 0x4D494450 and h[1] == len(lens) and h[3] == cp and h[2] == int(nchunks.sum())
     cptr = ws[ci:ci + 4 * (len(lens) + 1)].cpu().view(torch.int32).numpy()
     assert cptr.tolist() == [0] + np.cumsum(nchunks).tolist()
