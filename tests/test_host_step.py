@@ -112,6 +112,20 @@ def test_host_step_matches_python_loops(seed):
         assert _snapshot(a) == _snapshot(b), step
 
 
+def test_host_step_accepts_numpy_lengths():
+    a, b = _mgr(64), _mgr(64)
+    for m in (a, b):
+        for r in ("x", "y"):
+            m.add_request(r, ["main"])
+    entries = [("x", "main"), ("y", "main")]
+    sl = np.array([17, 3], dtype=np.int64)
+    ma = _py_meta(a, entries, [a.get_state(r, l) for r, l in entries], sl, a.state_generation)
+    mb = b.alloc_pack_meta(entries, [b.get_state(r, l) for r, l in entries], sl, b.state_generation)
+    assert np.array_equal(ma, mb)
+    hs.advance([b.get_state(r, l) for r, l in entries], sl, None)
+    assert [b.get_state(r, "main").seq_len for r in ("x", "y")] == [17, 3]
+
+
 def test_host_step_rejects_rows_longer_than_the_table():
     m = _mgr(600)
     m.add_request("x", ["main"])
