@@ -108,6 +108,21 @@ int mi_pack_plan(const int32_t* req_slot, const int32_t* seq_len, const int32_t*
                  int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, void* workspace,
                  int64_t workspace_bytes, void* stream);
 
+/* mi_pack_plan (workspace != NULL) or mi_pack (workspace == NULL) with the step's
+ * metadata in HOST memory, handed to the kernel as its launch argument instead of being
+ * copied to the device first: meta holds meta_len <= MI_PACK_HOST_META int32 values,
+ * [req_slot | seq_len | new_len | num_pages | table_pages] (batch values each, in that
+ * order) followed by the new pages; the buffer may be reused once the call returns.
+ * Same outputs as the device-pointer entry points.  Extension for small steps (no
+ * counterpart in the reference): it saves the host-to-device copy of the metadata. */
+#define MI_PACK_HOST_META 768
+int mi_pack_plan_host(const int32_t* meta, int32_t meta_len, int32_t batch, int32_t* block_table,
+                      int64_t block_table_stride, int32_t page_size, int32_t* qo_indptr,
+                      int32_t* kv_indptr, int32_t* kv_indices, int32_t* last_page_len,
+                      int64_t* kv_locations, int32_t grid_blocks, int32_t num_qo_heads,
+                      int32_t num_kv_heads, int32_t head_dim, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
 /* Incremental device block-table update: block_table[slot[i]*stride + pos[i]] = page[i]
  * for i < n.  Keeps the device copy of each request's page list in step with the
  * host allocator (mstar/engine/kv_store.py:463-482) without re-sending whole lists. */

@@ -85,6 +85,10 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _P, _P, _P, _I32, _P, _I64, _P, _P, _I32, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _I64, _P],
     ),
+    "mi_pack_plan_host": (
+        ctypes.c_int,
+        [_P, _I32, _I32, _P, _I64, _I32, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _I64, _P],
+    ),
     "mi_block_table_update": (ctypes.c_int, [_P, _I64, _P, _P, _P, _I32, _P]),
     "mi_decode_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32]),
     "mi_decode_plan": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _I64, _P]),
@@ -249,6 +253,9 @@ def _event_create(device: torch.device) -> int:
     if rc != 0:
         raise RuntimeError(f"hipEventCreateWithFlags failed with HIP error {rc}")
     return ev.value
+
+
+PACK_HOST_META = 768  # MI_PACK_HOST_META: int32 values of step metadata passed as a kernel argument
 
 
 class PinnedUploader:

@@ -212,9 +212,25 @@ class BatchedCacheManager:
         b = qo.shape[0] - 1
         if total_pages is None:
             total_pages = int(meta[3 * b:4 * b].sum())
-        dmeta = self._pack.upload(meta)
         bt = self.alloc_manager.block_table
         grid = max(1, min(256, (total_pages + 1023) // 1024))  # about one page per thread
+        if meta.size <= _lib.PACK_HOST_META:
+            # small step: the metadata travels as the kernel's argument, no copy to the device
+            meta = np.ascontiguousarray(meta, dtype=np.int32)
+            w = plan_wrapper
+            ws = w._workspace if w is not None else None
+            _lib.check(
+                _lib.lib().mi_pack_plan_host(
+                    meta.ctypes.data, meta.size, b, bt.table.data_ptr(), bt.stride, self.kv_cache_config.page_size,
+                    qo.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(), last.data_ptr(),
+                    loc.data_ptr() if loc is not None else None, grid,
+                    w.num_qo_heads if w is not None else 0, w.num_kv_heads if w is not None else 0,
+                    w.head_dim if w is not None else 0, ws.data_ptr() if ws is not None else None,
+                    ws.numel() * ws.element_size() if ws is not None else 0, _lib.stream_ptr(self.device)),
+                "mi_pack_plan_host",
+            )
+            return
+        dmeta = self._pack.upload(meta)
         base = dmeta.data_ptr()
         args = [base, base + 4 * b, base + 8 * b, base + 12 * b, b, bt.table.data_ptr(), bt.stride, base + 16 * b,
                 base + 20 * b, self.kv_cache_config.page_size, qo.data_ptr(), kv_indptr.data_ptr(),

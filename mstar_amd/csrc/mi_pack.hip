@@ -13,6 +13,8 @@
 // inter-block synchronisation; the flattening of kv_indices is then shared
 // by all workgroups (grid-stride over the batch's pages, one binary search
 // in LDS per page id; the grid is sized for about one page per thread).
+#include <cstring>
+
 #include "mi_common.h"
 #include "mi_internal.h"
 #include "mi_plan.h"
@@ -126,6 +128,36 @@ __global__ __launch_bounds__(kPackThreads) void pack_plan_kernel(PackParams p, P
   pack_body(p, blockIdx.x - 1, gridDim.x - 1);
 }
 
+// The step's metadata as a kernel argument (mi_pack_plan_host): up to
+// MI_PACK_HOST_META int32 values, [slot | seq_len | new_len | num_pages |
+// pages on the device] (batch each) followed by the new pages.
+struct HostMeta {
+  int32_t v[MI_PACK_HOST_META];
+};
+
+// pack_plan_kernel over the argument copy; with_plan == 0: pack only (no plan workgroup).
+__global__ __launch_bounds__(kPackThreads) void pack_plan_host_kernel(PackParams p, PlanParams pl, HostMeta m,
+                                                                      int32_t with_plan) {
+  const int32_t* base = m.v;
+  const int b = p.batch;
+  p.req_slot = base;
+  p.seq_len = base + b;
+  p.new_len = base + 2 * b;
+  p.num_pages = base + 3 * b;
+  p.table_pages = base + 4 * b;
+  p.new_pages = base + 5 * b;
+  if (with_plan) {
+    if (blockIdx.x == 0) {
+      pl.num_pages = base + 3 * b;
+      decode_plan_body(pl);
+      return;
+    }
+    pack_body(p, blockIdx.x - 1, gridDim.x - 1);
+  } else {
+    pack_body(p, blockIdx.x, gridDim.x);
+  }
+}
+
 __global__ __launch_bounds__(256) void block_table_update_kernel(int32_t* table, int64_t stride,
                                                                  const int32_t* slot, const int32_t* pos,
                                                                  const int32_t* page, int32_t n) {
@@ -199,6 +231,35 @@ extern "C" int mi_pack_plan(const int32_t* req_slot, const int32_t* seq_len, con
   if (st != MI_OK) return st;
   pl.num_pages = num_pages;  // the plan reads the step's page counts, not the pack's outputs
   hipLaunchKernelGGL(pack_plan_kernel, dim3(grid_blocks + 1), dim3(kPackThreads), 0, (hipStream_t)stream, pp, pl);
+  MI_CHECK_LAUNCH();
+  return MI_OK;
+}
+
+extern "C" int mi_pack_plan_host(const int32_t* meta, int32_t meta_len, int32_t batch, int32_t* block_table,
+                                 int64_t block_table_stride, int32_t page_size, int32_t* qo_indptr,
+                                 int32_t* kv_indptr, int32_t* kv_indices, int32_t* last_page_len,
+                                 int64_t* kv_locations, int32_t grid_blocks, int32_t num_qo_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
+  using namespace mi;
+  if (!meta || batch < 0 || meta_len < 5 * batch || meta_len > MI_PACK_HOST_META) return MI_ERR_INVALID;
+  HostMeta m;
+  memcpy(m.v, meta, sizeof(int32_t) * (size_t)meta_len);
+  // pointers for the argument checks only: the kernel points them at its copy of meta
+  const int32_t* chk = batch > 0 ? meta : nullptr;
+  PackParams pp{};
+  int st = pack_params(chk, chk, chk, chk, batch, block_table, block_table_stride, chk, chk, page_size, qo_indptr,
+                       kv_indptr, kv_indices, last_page_len, kv_locations, grid_blocks, &pp);
+  if (st != MI_OK) return st;
+  PlanParams pl{};
+  const int with_plan = workspace != nullptr;
+  if (with_plan) {
+    st = decode_plan_params(nullptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
+                            num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, 0, &pl);
+    if (st != MI_OK) return st;
+  }
+  hipLaunchKernelGGL(pack_plan_host_kernel, dim3(grid_blocks + with_plan), dim3(kPackThreads), 0,
+                     (hipStream_t)stream, pp, pl, m, with_plan);
   MI_CHECK_LAUNCH();
   return MI_OK;
 }

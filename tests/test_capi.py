@@ -239,3 +239,21 @@ def test_attention_entry_points_reject_unaligned_rows_on_the_host(L):
     far.page_stride = 2 * far.kv_stride
     assert L.mi_prefill_run(ok_q, 0, 4096, 128, ctypes.byref(far), p, p, p, p, 4, 64, 32, 1, 0.1, ws, 1 << 20,
                             ok_q, 4096, 128, None) == MI_ERR_UNSUPPORTED
+
+
+def test_pack_plan_host_arguments_are_checked(L):
+    """mi_pack_plan_host: the metadata size against the argument buffer, then mi_pack_plan's checks."""
+    meta = (ctypes.c_int32 * 1024)()
+    m = ctypes.cast(meta, ctypes.c_void_p)
+    buf = (ctypes.c_int32 * 64)()
+    p = ctypes.cast(buf, ctypes.c_void_p)
+
+    def call(meta_len=20, batch=4, grid=1, ws=p, meta_ptr=m):
+        return L.mi_pack_plan_host(meta_ptr, meta_len, batch, p, 8, 16, p, p, p, p, None, grid, 32, 4, 128, ws,
+                                   1 << 30, None)
+
+    assert call(meta_len=769) == MI_ERR_INVALID        # more than MI_PACK_HOST_META values
+    assert call(meta_len=19) == MI_ERR_INVALID         # fewer than 5 values per request
+    assert call(meta_ptr=None) == MI_ERR_INVALID       # no metadata
+    assert call(grid=0) == MI_ERR_INVALID              # pack: no workgroups
+    assert call(grid=0, ws=None) == MI_ERR_INVALID     # pack only: same checks

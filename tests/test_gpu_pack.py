@@ -152,6 +152,69 @@ def test_decode_plan_partition(gpu, lens, pool, hq, hkv):
     assert loc.cpu().tolist() == exp
 
 
+@pytest.mark.parametrize("with_plan", [True, False])
+def test_pack_plan_host_matches_device_metadata(gpu, with_plan):
+    """mi_pack_plan_host (metadata as the kernel argument) == mi_pack_plan / mi_pack with
+    the same metadata in device memory: packed arrays, table rows and plan."""
+    from mstar_amd.cache_manager import _step_tensors
+
+    ps, hq, hkv, d = 16, 24, 8, 128
+    rng = np.random.default_rng(11)
+    lens = [0, 1, 16, 17] + rng.integers(1, 3000, size=60).tolist()
+    b = len(lens)
+    npages = np.array([(t + ps - 1) // ps for t in lens], dtype=np.int32)
+    # a decode step: all but the last page or two of each list are already in the table
+    old = np.maximum(npages - rng.integers(0, 3, size=b), 0).astype(np.int32)
+    stride = int(npages.max()) + 1
+    pool = torch.randperm(int(npages.sum()) + 64, generator=torch.Generator().manual_seed(5)).numpy().astype(np.int32)
+    rows = np.zeros((b, stride), dtype=np.int32)
+    new_pages, off = [], 0
+    for r in range(b):
+        rows[r, :npages[r]] = pool[off:off + npages[r]]
+        new_pages.append(rows[r, old[r]:npages[r]])
+        off += npages[r]
+    meta = np.empty((5, b), dtype=np.int32)
+    meta[0] = rng.permutation(b)                 # slots
+    meta[1] = np.maximum(np.array(lens) - 1, 0)  # seq_len before the step
+    meta[2] = 1
+    meta[3] = npages
+    meta[4] = old
+    flat = np.concatenate([meta.reshape(-1)] + new_pages).astype(np.int32)
+    assert flat.size <= _lib.PACK_HOST_META
+    dmeta = torch.from_numpy(flat).to(gpu)
+    base = dmeta.data_ptr()
+    table0 = np.zeros((b, stride), dtype=np.int32)
+    for r in range(b):
+        table0[meta[0][r], :old[r]] = rows[r, :old[r]]
+    outs = []
+    for host in (False, True):
+        ws = workspace(gpu, 64 << 20)
+        ws.zero_()
+        table = torch.from_numpy(table0).to(gpu)
+        qo, ip, idx, last, loc = _step_tensors(b, int(npages.sum()), True, gpu)
+        wsp, wsn = (ws.data_ptr(), ws.numel()) if with_plan else (None, 0)
+        L = _lib.lib()
+        if host:
+            _lib.check(L.mi_pack_plan_host(flat.ctypes.data, flat.size, b, table.data_ptr(), stride, ps, qo.data_ptr(),
+                                           ip.data_ptr(), idx.data_ptr(), last.data_ptr(), loc.data_ptr(), 3, hq, hkv,
+                                           d, wsp, wsn, _lib.stream_ptr()), "pack_plan_host")
+        else:
+            args = [base, base + 4 * b, base + 8 * b, base + 12 * b, b, table.data_ptr(), stride, base + 16 * b,
+                    base + 20 * b, ps, qo.data_ptr(), ip.data_ptr(), idx.data_ptr(), last.data_ptr(), loc.data_ptr(), 3]
+            if with_plan:
+                _lib.check(L.mi_pack_plan(*args, hq, hkv, d, wsp, wsn, _lib.stream_ptr()), "pack_plan")
+            else:
+                _lib.check(L.mi_pack(*args, _lib.stream_ptr()), "pack")
+        torch.cuda.synchronize()
+        outs.append(([t.cpu().tolist() for t in (qo, ip, idx, last, loc)], table.cpu().tolist(),
+                     ws[:1 << 16].cpu().tolist() if with_plan else None))
+    assert outs[0] == outs[1]
+    # and the packed page lists are the requests' lists
+    ip_h, idx_h = np.array(outs[1][0][1]), np.array(outs[1][0][2])
+    for r in range(b):
+        assert idx_h[ip_h[r]:ip_h[r + 1]].tolist() == rows[r, :npages[r]].tolist()
+
+
 def test_pack_plan_matches_pack_then_plan(gpu):
     """mi_pack_plan (one launch) == mi_pack followed by mi_decode_plan on the packed arrays."""
     from mstar_amd.cache_manager import _step_tensors
