@@ -60,11 +60,21 @@ def _check_heads(num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size:
 
 
 class _Staging:
-    """Pinned host buffer for asynchronous index uploads, reused across plans."""
+    """Pinned host buffers for asynchronous index uploads, reused across plans.
+
+    Two buffers alternate, and each upload is one copy on a side stream of
+    its own, issued as soon as plan() is called: it runs beside whatever the
+    launch stream is still executing (the previous step's attention), and
+    the launch stream waits for it (an event) before the plan kernel.  On
+    one stream the copy would sit between the previous step's last kernel
+    and this step's plan kernel (about 20 us for c4's 166 KB of indices).
+    """
 
     def __init__(self):
-        self.buf: torch.Tensor | None = None
-        self.event: torch.cuda.Event | None = None
+        self.bufs: list = [None, None]
+        self.events: list = [None, None]
+        self.i = 0
+        self.stream: torch.cuda.Stream | None = None
 
     def upload(self, parts: list[torch.Tensor], device: torch.device,
                dests: list[torch.Tensor | None]) -> list[torch.Tensor]:
@@ -76,19 +86,33 @@ class _Staging:
         flat = [p.reshape(-1).view(torch.int32) if p.dtype == torch.int64 else p.reshape(-1) for p in parts]
         sizes = [f.numel() for f in flat]
         total = sum(sizes)
-        if self.buf is None or self.buf.numel() < total:
-            self.buf = torch.empty(max(total, 1 << 16), dtype=torch.int32, pin_memory=True)
-            self.event = None
-        if self.event is not None:
-            self.event.synchronize()
+        i = self.i
+        self.i ^= 1
+        if self.events[i] is not None:
+            self.events[i].synchronize()  # the copy that last read buffer i is done
+        buf = self.bufs[i]
+        if buf is None or buf.numel() < total:
+            buf = self.bufs[i] = torch.empty(max(total, 1 << 16), dtype=torch.int32, pin_memory=True)
         off = 0
         for f, n in zip(flat, sizes):
-            self.buf[off:off + n].copy_(f)
+            buf[off:off + n].copy_(f)
             off += n
-        staged = torch.empty(total, dtype=torch.int32, device=device)
-        staged.copy_(self.buf[:total], non_blocking=True)
-        self.event = torch.cuda.Event()
-        self.event.record()
+        cur = torch.cuda.current_stream(device)
+        if torch.cuda.is_current_stream_capturing():  # a captured plan keeps the copy on its own stream
+            staged = torch.empty(total, dtype=torch.int32, device=device)
+            staged.copy_(buf[:total], non_blocking=True)
+            ev = self.events[i] = torch.cuda.Event()
+            ev.record(cur)
+        else:
+            if self.stream is None or self.stream.device != cur.device:
+                self.stream = torch.cuda.Stream(device=device)
+            with torch.cuda.stream(self.stream):
+                staged = torch.empty(total, dtype=torch.int32, device=device)
+                staged.copy_(buf[:total], non_blocking=True)
+                ev = self.events[i] = torch.cuda.Event()
+                ev.record(self.stream)
+            cur.wait_event(ev)
+            staged.record_stream(cur)  # read on the launch stream from here on
         outs = []
         off = 0
         for p, f, n, d in zip(parts, flat, sizes, dests):
