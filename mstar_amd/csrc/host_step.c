@@ -11,8 +11,8 @@
  * as the specification; tests run both on the same state sequences.
  *
  * State attributes live in each instance's __dict__ (KVRequestState is a
- * plain dataclass) and are read and written there; an object without a
- * dict falls back to generic attribute access.
+ * plain dataclass) and are read and written there (CPython 3.10); an object
+ * without a dict, or a later interpreter, uses generic attribute access.
  */
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
@@ -22,8 +22,18 @@
 
 static PyObject *k_seq_len, *k_pos, *k_pages, *k_slot, *k_dev_list, *k_dev_len, *k_dev_ends;
 
+/* The instance dict is read directly on CPython 3.10 (the interpreter this
+ * package builds for); later versions keep instance attributes in their own
+ * layout, so there the generic attribute protocol is used. */
+#if PY_VERSION_HEX < 0x030B0000
+#define MI_DIRECT_DICT 1
+#else
+#define MI_DIRECT_DICT 0
+#endif
+
 /* New reference to attribute `k` of `o`, or NULL with an exception set. */
 static PyObject* get_attr(PyObject* o, PyObject* k) {
+#if MI_DIRECT_DICT
   PyObject** dp = _PyObject_GetDictPtr(o);
   if (dp && *dp) {
     PyObject* v = PyDict_GetItemWithError(*dp, k);
@@ -33,12 +43,15 @@ static PyObject* get_attr(PyObject* o, PyObject* k) {
     }
     if (PyErr_Occurred()) return NULL;
   }
+#endif
   return PyObject_GetAttr(o, k);
 }
 
 static int set_attr(PyObject* o, PyObject* k, PyObject* v) {
+#if MI_DIRECT_DICT
   PyObject** dp = _PyObject_GetDictPtr(o);
   if (dp && *dp) return PyDict_SetItem(*dp, k, v);
+#endif
   return PyObject_SetAttr(o, k, v);
 }
 
