@@ -53,7 +53,7 @@ struct PlanParams {
 constexpr int kSizeBuckets = 64;
 // Small jobs cut a request into at most this many items: its partials are
 // merged by one wavefront, one or two at a time.
-constexpr int kMaxSmallItems = 8;
+constexpr int kMaxSmallItems = 16;
 
 // One 1024-thread workgroup builds the plan.
 __device__ inline void decode_plan_body(const PlanParams& p) {

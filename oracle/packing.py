@@ -138,7 +138,7 @@ def decode_locations(kv_indptr, kv_indices, last_page_len) -> np.ndarray:
 
 def split_chunks(kv_indptr, page_size: int, target_units: int, num_kv_heads: int,
                  min_chunk_tokens: int = 1024, slots: int | None = None, small_chunk_tokens: int = 256,
-                 max_small_items: int = 8) -> tuple[int, np.ndarray]:
+                 max_small_items: int = 16) -> tuple[int, np.ndarray]:
     """Split-KV partition rule of the GPU plan: (item_pages, items per request).
 
     target = max(16, target_units // (4 * num_kv_heads)) (4 wavefronts per

@@ -188,10 +188,10 @@ def test_split_chunks_small_job_rule_against_brute_force():
         if ctarget >= cmin:
             assert cp == ctarget
             continue
-        lo = min(max(16, ctarget, -(-int(pages.max()) // 8), 1), cmin)
+        lo = min(max(16, ctarget, -(-int(pages.max()) // 16), 1), cmin)
         fits = [c for c in range(lo, cmin + 1) if cnt(c) <= slots]
         assert cp == (fits[0] if fits else cmin), (trial, pages.tolist(), slots, cp)
-        assert int(k.sum()) == cnt(cp) and all(-(-int(x) // cp) <= 8 or cp == cmin for x in pages)
+        assert int(k.sum()) == cnt(cp) and all(-(-int(x) // cp) <= 16 or cp == cmin for x in pages)
     # without slots the rule is the plain minimum chunk
     assert P.split_chunks(np.array([0, 5, 9]), 16, 4096, 4)[0] == 64
 
