@@ -51,8 +51,8 @@ struct PlanParams {
 // (request, index within the request, end page, items of the request); its
 // partial lives at chunk_indptr[request] + index whatever its list position.
 constexpr int kSizeBuckets = 64;
-// Small jobs cut a request into at most this many items: its partials are
-// merged by one wavefront, one or two at a time.
+// Small jobs cut a request into at most this many items: the merge of its
+// partials (one workgroup per request and kv-head) stays short.
 constexpr int kMaxSmallItems = 16;
 
 // One 1024-thread workgroup builds the plan.
