@@ -112,7 +112,8 @@ int mi_pack_plan(const int32_t* req_slot, const int32_t* seq_len, const int32_t*
  * metadata in HOST memory, handed to the kernel as its launch argument instead of being
  * copied to the device first: meta holds meta_len <= MI_PACK_HOST_META int32 values,
  * [req_slot | seq_len | new_len | num_pages | table_pages] (batch values each, in that
- * order) followed by the new pages; the buffer may be reused once the call returns.
+ * order) followed by the new pages (as many as the num_pages - table_pages differences
+ * add up to, else MI_ERR_INVALID); the buffer may be reused once the call returns.
  * Same outputs as the device-pointer entry points.  Extension for small steps (no
  * counterpart in the reference): it saves the host-to-device copy of the metadata. */
 #define MI_PACK_HOST_META 768

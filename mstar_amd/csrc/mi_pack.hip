@@ -242,7 +242,15 @@ extern "C" int mi_pack_plan_host(const int32_t* meta, int32_t meta_len, int32_t 
                                  int32_t num_kv_heads, int32_t head_dim, void* workspace, int64_t workspace_bytes,
                                  void* stream) {
   using namespace mi;
-  if (!meta || batch < 0 || meta_len < 5 * batch || meta_len > MI_PACK_HOST_META) return MI_ERR_INVALID;
+  if (!meta || batch < 0 || meta_len > MI_PACK_HOST_META || (int64_t)meta_len < 5LL * batch) return MI_ERR_INVALID;
+  // the new pages the kernel will read are exactly the ones meta carries
+  int64_t new_pages = 0;
+  for (int32_t r = 0; r < batch; ++r) {
+    const int32_t np = meta[3 * batch + r], old = meta[4 * batch + r];
+    if (np < 0 || old < 0) return MI_ERR_INVALID;
+    new_pages += np - (old < np ? old : np);
+  }
+  if (new_pages != (int64_t)meta_len - 5LL * batch) return MI_ERR_INVALID;
   HostMeta m;
   memcpy(m.v, meta, sizeof(int32_t) * (size_t)meta_len);
   // pointers for the argument checks only: the kernel points them at its copy of meta

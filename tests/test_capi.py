@@ -253,6 +253,9 @@ def test_pack_plan_host_arguments_are_checked(L):
                                    1 << 30, None)
 
     assert call(meta_len=769) == MI_ERR_INVALID        # more than MI_PACK_HOST_META values
+    meta[12] = 3                                       # request 0 holds 3 pages, none in the table:
+    assert call(meta_len=20) == MI_ERR_INVALID         # 3 new pages expected, none given
+    meta[12] = 0
     assert call(meta_len=19) == MI_ERR_INVALID         # fewer than 5 values per request
     assert call(meta_ptr=None) == MI_ERR_INVALID       # no metadata
     assert call(grid=0) == MI_ERR_INVALID              # pack: no workgroups
