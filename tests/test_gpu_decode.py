@@ -109,6 +109,24 @@ def test_decode_shapes(gpu, hq, hkv, d, ps):
     assert err < TOL_BF16
 
 
+@pytest.mark.parametrize("b,hq,hkv,max_len", [(1100, 8, 2, 64), (1300, 32, 4, 700)])
+def test_decode_batch_over_1024(gpu, b, hq, hkv, max_len):
+    """More requests than the plan workgroup's 1024 threads: the plan's scans, the
+    small-job search and the partition run over several windows of requests (short
+    contexts: a small job; longer ones: paired kv-heads and split requests)."""
+    rng = np.random.default_rng(b)
+    lens = rng.integers(1, max_len + 1, size=b).tolist()
+    ps = 16
+    pool = int(sum(-(-np.array(lens) // ps))) + 8
+    qo, kv_indptr, kv_indices, last = custom_batch(lens, ps, pool, seed=b)
+    log(f"decode B={b} hq={hq} hkv={hkv} max_len={max_len}")
+    hdr = []
+    out, ref = _run_decode(gpu, hq, hkv, 128, ps, kv_indptr, kv_indices, last, pool, seed=b, plan_header=hdr)
+    err = max_abs(out, ref)
+    log(f"  items={hdr[2]} item_pages={hdr[3]} max_abs={err:.3e}")
+    assert hdr[1] == b and err < TOL_BF16
+
+
 def test_decode_fp16_and_device_indices(gpu):
     qo, kv_indptr, kv_indices, last = custom_batch([5, 70, 700], 16, 64, seed=3)
     out, ref = _run_decode(gpu, 8, 2, 128, 16, kv_indptr, kv_indices, last, 64, seed=3, dtype=torch.float16,

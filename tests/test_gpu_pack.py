@@ -215,13 +215,17 @@ def test_pack_plan_host_matches_device_metadata(gpu, with_plan):
         assert idx_h[ip_h[r]:ip_h[r + 1]].tolist() == rows[r, :npages[r]].tolist()
 
 
-def test_pack_plan_matches_pack_then_plan(gpu):
-    """mi_pack_plan (one launch) == mi_pack followed by mi_decode_plan on the packed arrays."""
+@pytest.mark.parametrize("extra", [300, 1100])
+def test_pack_plan_matches_pack_then_plan(gpu, extra):
+    """mi_pack_plan (one launch) == mi_pack followed by mi_decode_plan on the packed arrays,
+    and the packed arrays are the closed-form ones; 1108 requests take the pack's and the
+    plan's loops over several 1024-request windows."""
     from mstar_amd.cache_manager import _step_tensors
 
     ps, hq, hkv, d = 16, 32, 4, 128
     rng = np.random.default_rng(7)
-    lens = [0, 1, 17, 300, 5000, 32768, 4096, 77] + rng.integers(1, 20000, size=300).tolist()
+    lens = [0, 1, 17, 300, 5000, 32768, 4096, 77] + rng.integers(1, 20000 if extra < 1024 else 2000,
+                                                                 size=extra).tolist()
     b = len(lens)
     npages = [(t + ps - 1) // ps for t in lens]
     pool = torch.randperm(sum(npages) + 64, generator=torch.Generator().manual_seed(3)).numpy().astype(np.int32)
@@ -260,5 +264,13 @@ def test_pack_plan_matches_pack_then_plan(gpu):
                      [t.cpu().tolist() for t in (qo, ip, idx, last, loc)], table.cpu().tolist()))
     (h0, c0, w0, o0, p0, t0), (h1, c1, w1, o1, p1, t1) = outs
     assert h0 == h1 and c0 == c1 and w0 == w1 and p0 == p1 and t0 == t1
+    # closed form (one new token per request; every page arrives with the step)
+    T = np.maximum(np.array(lens) - 1, 0) + 1  # seq_len before the step + the new token
+    np_ = np.array(npages)
+    want_ip = np.concatenate([[0], np.cumsum(np_)]).tolist()
+    want_last = np.where(T % ps == 0, ps, T % ps).tolist()
+    want_loc = [[int(pool[want_ip[r + 1] - 1]), want_last[r] - 1] if np_[r] else [-1, -1] for r in range(b)]
+    assert p0[0] == list(range(b + 1)) and p0[1] == want_ip and p0[2] == pool[:sum(npages)].tolist()
+    assert p0[3] == want_last and p0[4] == want_loc
     nfull = sum(1 for r, k, e, n in w0 if e == (k + 1) * h0[3])
     assert o0[:nfull] and sorted(map(tuple, o0[:nfull])) == sorted(map(tuple, o1[:nfull]))  # full items first in both
