@@ -112,6 +112,26 @@ def test_host_step_matches_python_loops(seed):
         assert _snapshot(a) == _snapshot(b), step
 
 
+def test_host_step_matches_python_loops_at_large_batch():
+    a, b = _mgr(40000), _mgr(40000)
+    rng = random.Random(9)
+    rids = [f"r{i}" for i in range(1100)]
+    for m in (a, b):
+        for r in rids:
+            m.add_request(r, ["main"])
+    entries = [(r, "main") for r in rids]
+    for step in range(3):
+        sl = [rng.randint(1, 40) if step == 0 else 1 for _ in rids]
+        sa = [a.get_state(r, "main") for r in rids]
+        sb = [b.get_state(r, "main") for r in rids]
+        ma = _py_meta(a, entries, sa, sl, a.state_generation)
+        mb = b.alloc_pack_meta(entries, sb, sl, b.state_generation)
+        assert np.array_equal(ma, mb)
+        _advance_py(sa, sl, None)
+        hs.advance(sb, sl, None)
+        assert _snapshot(a) == _snapshot(b)
+
+
 def test_host_step_accepts_numpy_lengths():
     a, b = _mgr(64), _mgr(64)
     for m in (a, b):
