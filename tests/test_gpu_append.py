@@ -46,6 +46,23 @@ def test_append_bit_exact(gpu, src, dst):
     assert torch.equal(got, exp)
 
 
+@pytest.mark.parametrize("hkv,d", [(3, 72), (6, 128), (4, 96), (1, 256)])
+def test_append_head_shapes(gpu, hkv, d):
+    """Thread-to-element mapping for head counts and head_dims whose 8-element groups
+    per token are not a power of two (the append accepts any head_dim divisible by 8)."""
+    pool, ps, n = 24, 16, 200
+    page, slot, g = _case(2, n, pool, ps, hkv, d)
+    k = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, hkv, d, generator=g).to(torch.bfloat16)
+    cache_cpu = torch.zeros(pool, 2, ps, hkv, d, dtype=torch.bfloat16)
+    A.append(cache_cpu, page, slot, k, v)
+    cache = torch.zeros(pool, 2, ps, hkv, d, dtype=torch.bfloat16, device=gpu)
+    _append(cache, k.to(gpu), v.to(gpu), page.to(gpu), slot.to(gpu).data_ptr(), 1, n, None, None, None)
+    torch.cuda.synchronize()
+    log(f"append hkv={hkv} d={d}")
+    assert torch.equal(cache.cpu().view(torch.uint8), cache_cpu.view(torch.uint8))
+
+
 def test_append_skips_out_of_range_and_device_count(gpu):
     pool, ps, hkv, d = 8, 16, 2, 64
     k = torch.randn(5, hkv, d).to(torch.bfloat16).to(gpu)
