@@ -23,6 +23,7 @@ prefill partition on the GPU from those device tensors.
 
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass
 
 import numpy as np
@@ -35,6 +36,20 @@ from .rope import apply_llama31_rope_pos_ids_inplace, apply_rope_pos_ids_inplace
 from .trace import trace_range
 
 _LLAMA31_KEYS = ("low_freq_factor", "high_freq_factor", "old_context_len")
+
+
+@contextlib.contextmanager
+def _unsynced_on_error(states: list[KVRequestState]):
+    """If planning fails between the allocation and the queued pack launch,
+    the states' new pages may be marked as on the device without having
+    reached the block table: mark them unsynced so the next step resends
+    their whole page lists."""
+    try:
+        yield
+    except BaseException:
+        for st in states:
+            st.pages_changed()
+        raise
 
 
 @dataclass
@@ -214,37 +229,36 @@ class BatchedCacheManager:
             total_pages = int(meta[3 * b:4 * b].sum())
         bt = self.alloc_manager.block_table
         grid = max(1, min(256, (total_pages + 1023) // 1024))  # about one page per thread
+        stream = _lib.stream_ptr(self.device)
+        w = plan_wrapper
+        ws = w._workspace if w is not None else None
+        plan_args = (w.num_qo_heads if w is not None else 0, w.num_kv_heads if w is not None else 0,
+                     w.head_dim if w is not None else 0, ws.data_ptr() if ws is not None else None,
+                     ws.numel() * ws.element_size() if ws is not None else 0)
+        loc_ptr = loc.data_ptr() if loc is not None else None
+        ps = self.kv_cache_config.page_size
         if meta.size <= _lib.PACK_HOST_META:
             # small step: the metadata travels as the kernel's argument, no copy to the device
             meta = np.ascontiguousarray(meta, dtype=np.int32)
-            w = plan_wrapper
-            ws = w._workspace if w is not None else None
-            _lib.check(
+            bt.launch(lambda table: _lib.check(
                 _lib.lib().mi_pack_plan_host(
-                    meta.ctypes.data, meta.size, b, bt.table.data_ptr(), bt.stride, self.kv_cache_config.page_size,
-                    qo.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(), last.data_ptr(),
-                    loc.data_ptr() if loc is not None else None, grid,
-                    w.num_qo_heads if w is not None else 0, w.num_kv_heads if w is not None else 0,
-                    w.head_dim if w is not None else 0, ws.data_ptr() if ws is not None else None,
-                    ws.numel() * ws.element_size() if ws is not None else 0, _lib.stream_ptr(self.device)),
-                "mi_pack_plan_host",
-            )
+                    meta.ctypes.data, meta.size, b, table, bt.stride, ps, qo.data_ptr(), kv_indptr.data_ptr(),
+                    kv_indices.data_ptr(), last.data_ptr(), loc_ptr, grid, *plan_args, stream),
+                "mi_pack_plan_host"))
             return
         dmeta = self._pack.upload(meta)
         base = dmeta.data_ptr()
-        args = [base, base + 4 * b, base + 8 * b, base + 12 * b, b, bt.table.data_ptr(), bt.stride, base + 16 * b,
-                base + 20 * b, self.kv_cache_config.page_size, qo.data_ptr(), kv_indptr.data_ptr(),
-                kv_indices.data_ptr(), last.data_ptr(), loc.data_ptr() if loc is not None else None, grid]
-        if plan_wrapper is None:
-            _lib.check(_lib.lib().mi_pack(*args, _lib.stream_ptr(self.device)), "mi_pack")
-            return
-        w = plan_wrapper
-        ws = w._workspace
-        _lib.check(
-            _lib.lib().mi_pack_plan(*args, w.num_qo_heads, w.num_kv_heads, w.head_dim, ws.data_ptr(),
-                                    ws.numel() * ws.element_size(), _lib.stream_ptr(self.device)),
-            "mi_pack_plan",
-        )
+
+        def pack(table):
+            args = [base, base + 4 * b, base + 8 * b, base + 12 * b, b, table, bt.stride, base + 16 * b,
+                    base + 20 * b, ps, qo.data_ptr(), kv_indptr.data_ptr(), kv_indices.data_ptr(), last.data_ptr(),
+                    loc_ptr, grid]
+            if w is None:
+                _lib.check(_lib.lib().mi_pack(*args, stream), "mi_pack")
+            else:
+                _lib.check(_lib.lib().mi_pack_plan(*args, *plan_args, stream), "mi_pack_plan")
+
+        bt.launch(pack)
 
     def _plan_attention_impl(self, seq_lens, dtype, is_causal, write_store, label) -> None:
         assert self.kv_cache is not None
@@ -255,51 +269,52 @@ class BatchedCacheManager:
         b = len(self.request_ids)
         nv = self.enable_nvtx
         # host side: FIFO allocation and the block-table delta (the reference builds its page lists here)
-        with trace_range(nv, "cache.plan_attention.build_lists"):
-            entries, states, gen = self._label_states(label)
-            meta = self._alloc_entries(entries, seq_lens, states, gen)
-        total_pages = int(meta[3 * b:4 * b].sum())
-        new_lens = meta[2 * b:3 * b]
-        is_decode = bool((new_lens == 1).all())
+        entries, states, gen = self._label_states(label)
+        with _unsynced_on_error(states):
+            with trace_range(nv, "cache.plan_attention.build_lists"):
+                meta = self._alloc_entries(entries, seq_lens, states, gen)
+            total_pages = int(meta[3 * b:4 * b].sum())
+            new_lens = meta[2 * b:3 * b]
+            is_decode = bool((new_lens == 1).all())
 
-        ps = self._plan_states.get(label)
-        if ps is not None and ps.wrapper is not None:
-            wrapper = ps.wrapper
-        else:
-            cls = PagedDecodeWrapper if is_decode else PagedPrefillWrapper
-            wrapper = cls(
-                workspace_buffer=self.buffer_manager.get(label),
-                num_qo_heads=cfg.num_qo_heads,
-                num_kv_heads=cfg.num_kv_heads,
-                head_dim=cfg.head_dim,
-                page_size=ps_,
-                device=self.device,
-                enable_nvtx=self.enable_nvtx,
-            )
-            ps = _PlanState(wrapper=wrapper)
-            self._plan_states[label] = ps
+            ps = self._plan_states.get(label)
+            if ps is not None and ps.wrapper is not None:
+                wrapper = ps.wrapper
+            else:
+                cls = PagedDecodeWrapper if is_decode else PagedPrefillWrapper
+                wrapper = cls(
+                    workspace_buffer=self.buffer_manager.get(label),
+                    num_qo_heads=cfg.num_qo_heads,
+                    num_kv_heads=cfg.num_kv_heads,
+                    head_dim=cfg.head_dim,
+                    page_size=ps_,
+                    device=self.device,
+                    enable_nvtx=self.enable_nvtx,
+                )
+                ps = _PlanState(wrapper=wrapper)
+                self._plan_states[label] = ps
 
-        # device: one upload of [slot | seq_len | new_len | num_pages], one pack kernel
-        graph_static = isinstance(wrapper, PagedDecodeWrapper) and wrapper.use_cuda_graph
-        graph_static_pf = isinstance(wrapper, PagedPrefillWrapper) and wrapper.use_cuda_graph
-        if graph_static or graph_static_pf:
-            qo = wrapper._qo_indptr_buf if graph_static_pf else torch.empty(b + 1, dtype=torch.int32, device=self.device)
-            kv_indptr = wrapper._paged_kv_indptr_buf
-            kv_indices = wrapper._paged_kv_indices_buf
-            last = wrapper._paged_kv_last_page_len_buf
-            if total_pages > kv_indices.shape[0]:
-                raise ValueError(f"{total_pages} pages > wrapper max_num_pages {kv_indices.shape[0]}")
-            loc = None
-            if is_decode:
-                loc = wrapper.kv_cache_locations if graph_static and b == wrapper.batch_size else \
-                    torch.empty(b, 2, dtype=torch.long, device=self.device)
-        else:
-            qo, kv_indptr, kv_indices, last, loc = _step_tensors(b, total_pages, is_decode, self.device)
-        fused = isinstance(wrapper, PagedDecodeWrapper) and is_decode and (not graph_static or b == wrapper.batch_size)
-        # device side: one upload of the step's metadata and one pack launch (the reference's torch.tensor builds)
-        with trace_range(nv, "cache.plan_attention.make_tensors"):
-            self._launch_pack(meta, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=wrapper if fused else None,
-                              total_pages=total_pages)
+            # device: one upload of [slot | seq_len | new_len | num_pages], one pack kernel
+            graph_static = isinstance(wrapper, PagedDecodeWrapper) and wrapper.use_cuda_graph
+            graph_static_pf = isinstance(wrapper, PagedPrefillWrapper) and wrapper.use_cuda_graph
+            if graph_static or graph_static_pf:
+                qo = wrapper._qo_indptr_buf if graph_static_pf else torch.empty(b + 1, dtype=torch.int32, device=self.device)
+                kv_indptr = wrapper._paged_kv_indptr_buf
+                kv_indices = wrapper._paged_kv_indices_buf
+                last = wrapper._paged_kv_last_page_len_buf
+                if total_pages > kv_indices.shape[0]:
+                    raise ValueError(f"{total_pages} pages > wrapper max_num_pages {kv_indices.shape[0]}")
+                loc = None
+                if is_decode:
+                    loc = wrapper.kv_cache_locations if graph_static and b == wrapper.batch_size else \
+                        torch.empty(b, 2, dtype=torch.long, device=self.device)
+            else:
+                qo, kv_indptr, kv_indices, last, loc = _step_tensors(b, total_pages, is_decode, self.device)
+            fused = isinstance(wrapper, PagedDecodeWrapper) and is_decode and (not graph_static or b == wrapper.batch_size)
+            # device side: one upload of the step's metadata and one pack launch (the reference's torch.tensor builds)
+            with trace_range(nv, "cache.plan_attention.make_tensors"):
+                self._launch_pack(meta, qo, kv_indptr, kv_indices, last, loc, plan_wrapper=wrapper if fused else None,
+                                  total_pages=total_pages)
         self._last_pack = (qo, kv_indptr, kv_indices[:total_pages], last, loc)
         with trace_range(nv, "cache.plan_attention.wrapper_plan"):
             if fused:
@@ -326,14 +341,17 @@ class BatchedCacheManager:
         cfg = self.kv_cache_config
         entries = [(rid, label) for label in labels for rid in self.request_ids]
         sls = [int(seq_lens[i]) for _ in labels for i in range(len(self.request_ids))]
-        meta = self._alloc_entries(entries, sls)
-        n = len(entries)
-        total_pages = int(meta[3 * n:4 * n].sum())
-        qo = torch.empty(n + 1, dtype=torch.int32, device=self.device)
-        kv_indptr = torch.empty(n + 1, dtype=torch.int32, device=self.device)
-        kv_indices = torch.empty(max(total_pages, 1), dtype=torch.int32, device=self.device)
-        last = torch.empty(n, dtype=torch.int32, device=self.device)
-        self._launch_pack(meta, qo, kv_indptr, kv_indices, last, None)
+        generation = self.alloc_manager.state_generation
+        states = [self._get_state(rid, label) for rid, label in entries]
+        with _unsynced_on_error(states):
+            meta = self._alloc_entries(entries, sls, states, generation)
+            n = len(entries)
+            total_pages = int(meta[3 * n:4 * n].sum())
+            qo = torch.empty(n + 1, dtype=torch.int32, device=self.device)
+            kv_indptr = torch.empty(n + 1, dtype=torch.int32, device=self.device)
+            kv_indices = torch.empty(max(total_pages, 1), dtype=torch.int32, device=self.device)
+            last = torch.empty(n, dtype=torch.int32, device=self.device)
+            self._launch_pack(meta, qo, kv_indptr, kv_indices, last, None)
         self._last_pack = (qo, kv_indptr, kv_indices[:total_pages], last, None)
         wrapper = PagedPrefillWrapper(
             workspace_buffer=self.buffer_manager.get(combined_label),

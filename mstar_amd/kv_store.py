@@ -5,8 +5,9 @@ Host side mirrors M*'s ``mstar/engine/kv_store.py``:
 * :class:`PageAllocator` — FIFO free list (``kv_store.py:25-67``): pages start
   in order ``0..N-1``, allocation pops from the head, ``free`` appends to the
   tail.  Page ids therefore depend on batch order exactly as in the reference.
-* :class:`KVCacheConfig`, :class:`KVRequestState`, :class:`AllocationFailedError`
-  (``kv_store.py:70-154``).
+* :class:`KVCacheConfig`, :class:`PositionInfo`, :class:`KVRequestState`,
+  :class:`AllocationFailedError`, :class:`TransferEngineInfo`,
+  :class:`StoreWritePolicy` (``kv_store.py:70-175``).
 * :class:`PagedAllocationManager` — ``kv_store.py:394-660``: allocation and
   request state (``alloc``, ``get_state``, ``add_request``, ``remove_request``,
   ``reset_label``), remote reads (``start_async_retrieve``, ``sync_retrieve``,
@@ -28,8 +29,10 @@ without the reference's per-step re-flattening of every page list on the host
 from __future__ import annotations
 
 import collections
+import enum
 import threading
 from dataclasses import dataclass, field
+from typing import Any
 
 import numpy as np
 import torch
@@ -95,6 +98,14 @@ class KVCacheConfig:
         self.original_num_kv_heads = self.num_kv_heads
         self.original_num_qo_heads = self.num_qo_heads
 
+    def get_node_str(self) -> str:
+        """Key of this cache among an engine's caches (``kv_store.py:90-93``):
+        the node names joined by ``///``, or ``ALL_NODES`` when the config
+        lists none."""
+        if self.nodes is None:
+            return "ALL_NODES"
+        return "///".join(self.nodes)
+
     def shard(self, tp_size: int):
         """Head sharding for tensor parallelism (``kv_store.py:95-101``)."""
         if tp_size >= self.original_num_kv_heads:
@@ -107,6 +118,14 @@ class KVCacheConfig:
             raise ValueError(f"{self.original_num_qo_heads} q heads do not split over {tp_size}")
         self.num_qo_heads = self.original_num_qo_heads // tp_size
         self._sharded = True
+
+
+@dataclass
+class PositionInfo:
+    """What a model's ``prepare_inputs`` reads of one label (``kv_store.py:105-108``)."""
+
+    full_seq_len: int = 0
+    position_id_start: int = 0
 
 
 @dataclass
@@ -134,6 +153,10 @@ class KVRequestState:
     _dev_len: int = field(default=0, repr=False, compare=False)
     _dev_ends: tuple = field(default=(-1, -1), repr=False, compare=False)
 
+    def get_pos_info(self) -> PositionInfo:
+        """Sequence length and first position id (``kv_store.py:123-127``)."""
+        return PositionInfo(full_seq_len=self.seq_len, position_id_start=self.position_id_start)
+
     def pages_changed(self) -> None:
         """Mark ``page_indices`` as edited in place: the next sync resends all of it."""
         self._dev_list = None
@@ -153,6 +176,23 @@ class AllocationFailedError(RuntimeError):
         self.label = label
 
 
+@dataclass
+class TransferEngineInfo:
+    """The worker's tensor transport, as the engine hands it to the
+    allocation manager (``kv_store.py:164-168``)."""
+
+    my_entity_id: str
+    my_session_id: str
+    transfer_engine: Any
+
+
+class StoreWritePolicy(enum.Enum):
+    """Whether a worker's KV may be read elsewhere (``kv_store.py:171-174``)."""
+
+    ALWAYS = "always"
+    NEVER = "never"
+
+
 class DeviceBlockTable:
     """HBM copy of the page lists of live request states.
 
@@ -168,6 +208,7 @@ class DeviceBlockTable:
         self.stride = int(max_pages_per_seq)
         self.table = torch.zeros(max_slots, self.stride, dtype=torch.int32, device=self.device)
         self._free_slots = list(range(max_slots - 1, -1, -1))
+        self._retired: list[torch.Tensor] = []
         self._lock = threading.Lock()
         self._staging: torch.Tensor | None = None
         self._staging_event: torch.cuda.Event | None = None
@@ -177,12 +218,17 @@ class DeviceBlockTable:
         return self.table.shape[0]
 
     def _grow(self) -> None:
-        """Double the table.  Pack and update kernels on any stream may still
-        read or write the old table: the device is drained before the copy and
-        after it, so the copy sees every earlier write and the old block is
-        not reused before the copy has read it.  Growth only happens when
-        more states are live than the table has rows (it starts at
-        ``max_slots``), never under graph capture (planning is not captured)."""
+        """Double the table (called with ``_lock`` held).  Every launch that
+        reads or writes the table takes ``_lock`` from reading
+        ``table.data_ptr()`` until the launch is queued (:meth:`launch`), so
+        no launch can pick up the old table after this swap; launches queued
+        before it are drained by the device synchronisation before the copy,
+        and the copy itself by the one after it.  The old tensor is kept
+        (``_retired``) until the table is dropped, so even a launch made
+        outside that protocol cannot write into memory handed out again.
+        Growth only happens when more states are live than the table has
+        rows (it starts at ``max_slots``), never under graph capture
+        (planning is not captured)."""
         old = self.table
         on_gpu = self.device.type == "cuda"
         if on_gpu:
@@ -192,8 +238,16 @@ class DeviceBlockTable:
         table[: old.shape[0]].copy_(old)
         if on_gpu:
             torch.cuda.synchronize(self.device)
+        self._retired.append(old)
         self.table = table
         self._free_slots = list(range(new_slots - 1, old.shape[0] - 1, -1)) + self._free_slots
+
+    def launch(self, fn):
+        """``fn(table_ptr)`` with the table lock held: for the kernels that
+        read or write the table, so the pointer they get stays the live table
+        until they are queued (see :meth:`_grow`)."""
+        with self._lock:
+            return fn(self.table.data_ptr())
 
     def acquire(self, state: KVRequestState) -> int:
         with self._lock:
@@ -280,33 +334,36 @@ class DeviceBlockTable:
                 new)
 
     def sync(self, states: list[KVRequestState], stream: torch.cuda.Stream | None = None) -> None:
-        """Bring the device rows of ``states`` up to date (async on ``stream``)."""
+        """Bring the device rows of ``states`` up to date (async on ``stream``).
+        If the update cannot be queued, the states are marked unsynced again."""
         slots, poss, pages = [], [], []
-        for st in states:
-            slot = self.acquire(st)
-            pl = st.page_indices
-            n = len(pl)
-            if n > self.stride:
-                raise ValueError(f"request holds {n} pages, block table rows hold {self.stride}")
-            start = self._synced_prefix(st, pl, n)
-            if n > start:
-                slots.append(np.full(n - start, slot, dtype=np.int32))
-                poss.append(np.arange(start, n, dtype=np.int32))
-                pages.append(np.asarray(pl[start:], dtype=np.int32))
-            self._mark_synced(st, pl, n)
-        if not slots:
-            return
-        upd = np.concatenate([np.concatenate(slots), np.concatenate(poss), np.concatenate(pages)])
-        m = upd.size // 3
-        dev = self._upload(upd, stream)
-        st_ptr = (stream or torch.cuda.current_stream(self.device)).cuda_stream
-        base = dev.data_ptr()
-        _lib.check(
-            _lib.lib().mi_block_table_update(
-                self.table.data_ptr(), self.stride, base, base + 4 * m, base + 8 * m, m, st_ptr
-            ),
-            "mi_block_table_update",
-        )
+        try:
+            for st in states:
+                slot = self.acquire(st)
+                pl = st.page_indices
+                n = len(pl)
+                if n > self.stride:
+                    raise ValueError(f"request holds {n} pages, block table rows hold {self.stride}")
+                start = self._synced_prefix(st, pl, n)
+                if n > start:
+                    slots.append(np.full(n - start, slot, dtype=np.int32))
+                    poss.append(np.arange(start, n, dtype=np.int32))
+                    pages.append(np.asarray(pl[start:], dtype=np.int32))
+                self._mark_synced(st, pl, n)
+            if not slots:
+                return
+            upd = np.concatenate([np.concatenate(slots), np.concatenate(poss), np.concatenate(pages)])
+            m = upd.size // 3
+            dev = self._upload(upd, stream)
+            st_ptr = (stream or torch.cuda.current_stream(self.device)).cuda_stream
+            base = dev.data_ptr()
+            self.launch(lambda table: _lib.check(
+                _lib.lib().mi_block_table_update(table, self.stride, base, base + 4 * m, base + 8 * m, m, st_ptr),
+                "mi_block_table_update"))
+        except BaseException:
+            for st in states:
+                st.pages_changed()
+            raise
 
     def _upload(self, arr: np.ndarray, stream) -> torch.Tensor:
         """Async H2D of a small int32 array through a reused pinned buffer."""
@@ -328,18 +385,41 @@ class DeviceBlockTable:
 
 
 class PagedAllocationManager:
-    """Page allocation and per-request state (``kv_store.py:394-614``, attention subset).
+    """Page allocation and per-request state (``kv_store.py:394-660``).
 
-    ``device`` enables the :class:`DeviceBlockTable` used by the GPU packer.
+    Constructed as the reference engine constructs it
+    (``kv_cache_engine.py:150-157``: ``config``, ``kv_cache``,
+    ``transfer_engine_info``).  The transport in ``transfer_engine_info``
+    selects the KV reader the way ``kv_store.py:413-426`` does:
+
+    * ``None``, the reference's ``LocalTransferEngine``, or any transport
+      whose ``get_async_reader(device)`` returns None (single node: the
+      producer's pool is device-addressable) -> a
+      :class:`mstar_amd.kv_transfer.DeviceKVTransferEngine` over ``kv_cache``,
+      built on first use;
+    * an object that already is a KV reader (has ``read_pages_async``) ->
+      used as it is;
+    * anything else, e.g. the Mooncake RDMA transport, -> ``ValueError``, as
+      the reference raises for a transport it does not support: cross-node
+      RDMA page reads are outside this library (a transport can move the
+      buffers of :func:`mstar_amd.kv_transfer.pack_wire` instead).
+
+    Keyword extensions: ``device`` places the :class:`DeviceBlockTable` the
+    GPU packer reads (default: ``kv_cache``'s device when it is a GPU
+    tensor); ``transfer_engine`` passes a KV reader directly.
     """
 
     def __init__(self, config: KVCacheConfig, kv_cache: torch.Tensor | None = None,
+                 transfer_engine_info: TransferEngineInfo | None = None, *,
                  device: torch.device | str | None = None, transfer_engine=None):
         self.config = config
+        if transfer_engine is None and transfer_engine_info is not None:
+            transfer_engine = self._reader_for(transfer_engine_info, kv_cache)
         self._kv_transfer_engine = transfer_engine
         self.page_allocator = PageAllocator(config.max_num_pages)
         self.request_states: dict[str, dict[str, KVRequestState]] = {}
         self.kv_cache = kv_cache
+        self.write_policy = StoreWritePolicy.ALWAYS
         self.pending_reads: dict[str, dict[str, list]] = {}
         self._lock = threading.RLock()
         # Bumped whenever a state object is created or a request removed, so
@@ -351,6 +431,24 @@ class PagedAllocationManager:
         if device is not None:
             max_pages_per_seq = (config.max_seq_len + config.page_size - 1) // config.page_size
             self.block_table = DeviceBlockTable(max_pages_per_seq, torch.device(device))
+
+    @staticmethod
+    def _reader_for(info: TransferEngineInfo, kv_cache: torch.Tensor | None):
+        """The KV reader for ``info.transfer_engine`` (None: build the device
+        reader on first use); see the class docstring."""
+        te = info.transfer_engine
+        if te is None:
+            return None
+        if hasattr(te, "read_pages_async"):
+            return te
+        if type(te).__name__ == "LocalTransferEngine":
+            return None
+        reader = getattr(te, "get_async_reader", None)
+        if reader is not None and reader(kv_cache.device if kv_cache is not None else None) is None:
+            return None
+        raise ValueError(
+            f"Unsupported transfer engine type: {type(te)} (remote page reads over RDMA are outside this "
+            "library; single-node transports and device-addressable pools are supported)")
 
     @property
     def num_free_pages(self) -> int:
@@ -472,6 +570,12 @@ class PagedAllocationManager:
                 if self.block_table is not None:
                     self.block_table.release(old)
             self.request_states[request_id][label] = self._new_state()
+
+    def cleanup(self) -> None:
+        """Shut the KV reader down at engine shutdown (``kv_store.py:592-593``):
+        reads still in flight land first."""
+        if self._kv_transfer_engine is not None:
+            self._kv_transfer_engine.shutdown()
 
     def add_request(self, request_id: str, labels: list[str] | None = None) -> None:
         labels = labels or []
