@@ -286,10 +286,27 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     }
     // ---- S^T = K . Q^T  (A fragment: row col, elements 8*grp + 32*st .. +8)
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (PAIR) {
+      // One accumulator per head of the pair (k-steps [0, KS/2) are head 2h's
+      // elements, [KS/2, KS) head 2h+1's); each column keeps its own head's,
+      // so a non-finite key of one head never reaches the other head's scores
+      // through 0 * Inf.
+      f32x4 s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int st = 0; st < KS; ++st) {
-      const uint4 a = *(const uint4*)(kst + col * KRS + (8 * grp + 32 * st) * 2);
-      s = MT::mma_16x16x32(a, qf[st], s);
+      for (int st = 0; st < KS / 2; ++st) {
+        const uint4 a0 = *(const uint4*)(kst + col * KRS + (8 * grp + 32 * st) * 2);
+        const uint4 a1 = *(const uint4*)(kst + col * KRS + (8 * grp + 32 * (st + KS / 2)) * 2);
+        s = MT::mma_16x16x32(a0, qf[st], s);
+        s1 = MT::mma_16x16x32(a1, qf[st + KS / 2], s1);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = half ? s1[r] : s[r];
+    } else {
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        const uint4 a = *(const uint4*)(kst + col * KRS + (8 * grp + 32 * st) * 2);
+        s = MT::mma_16x16x32(a, qf[st], s);
+      }
     }
     float sv[4];
 #pragma unroll
@@ -432,7 +449,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
       o[i].w += sc[w] * v.w;
     }
   }
-  const float inv = L > 0.f ? vscale / L : 0.f;
+  const float inv = L > 0.f ? vscale / L : (L == 0.f ? 0.f : __builtin_nanf(""));  // NaN L: keep the row NaN
   if (!row_valid) return;
   if (nitems_b == 1) {
     // elements j of output row 4*grp + wave: dims dim_of(RUN, 4*grp + wave, j), row col
@@ -462,7 +479,10 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int i = 0; i < NS; ++i)
       *(float4*)(ob + 256 * (wave * NS + i)) = make_float4(o[i].x * inv, o[i].y * inv, o[i].z * inv, o[i].w * inv);
-    if (wave == 0 && grp == 0) p.lse_part[unit_idx * kRows + col] = L > 0.f ? M + fast_log2(L) : kNegInf;
+    // lse: -inf for an empty partial; NaN when the row met a NaN or +inf score,
+    // so the merge propagates it as a single softmax over the keys would.
+    if (wave == 0 && grp == 0)
+      p.lse_part[unit_idx * kRows + col] = L > 0.f ? M + fast_log2(L) : (L == 0.f ? kNegInf : __builtin_nanf(""));
   }
 }
 
@@ -526,7 +546,7 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (!(w[u] > kNegInf)) continue;  // past the end, or an empty partial
+      if (w[u] == kNegInf) continue;  // past the end, or an empty partial (a NaN lse makes the row NaN)
       if (w[u] > M) {
         const float sc = fast_exp2(M - w[u]);  // 0 while M is -inf
         wsum *= sc;

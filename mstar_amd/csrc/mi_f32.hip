@@ -308,7 +308,7 @@ __global__ __launch_bounds__(256) void attend_f32_kernel(DecodeParams p, F32Tile
       o[i].w += sc[w] * v.w;
     }
   }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const float inv = L > 0.f ? 1.f / L : (L == 0.f ? 0.f : __builtin_nanf(""));  // NaN L: keep the row NaN
   if (!row_valid) return;
   if (nitems_b == 1) {  // dims dim_of(RUN, 4*grp + wave, j) of row col
     float* dst = (float*)p.out + (int64_t)(qo_start + qtok) * p.out_stride_tok +
@@ -322,7 +322,8 @@ __global__ __launch_bounds__(256) void attend_f32_kernel(DecodeParams p, F32Tile
 #pragma unroll
     for (int i = 0; i < NV; ++i)
       *(float4*)(ob + 256 * (wave * NV + i)) = make_float4(o[i].x * inv, o[i].y * inv, o[i].z * inv, o[i].w * inv);
-    if (wave == 0 && grp == 0) p.lse_part[unit_idx * kRows + col] = L > 0.f ? M + fast_log2(L) : kNegInf;
+    if (wave == 0 && grp == 0)  // -inf: empty partial; NaN: the row met a NaN or +inf score
+      p.lse_part[unit_idx * kRows + col] = L > 0.f ? M + fast_log2(L) : (L == 0.f ? kNegInf : __builtin_nanf(""));
   }
 }
 

@@ -19,7 +19,9 @@ SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t w
 // Decode over head_dim 128 with at most 8 query heads per kv-head reads two
 // adjacent kv-heads as one 256-element row (512 contiguous bytes of a token
 // row instead of 256): each query row takes the 128 elements of its own head
-// and zeros in the other half, so its scores see only its head, and it keeps
+// and zeros in the other half, the score MFMAs accumulate the two halves in
+// separate registers and each row keeps its own head's (so its scores see
+// only its head, non-finite keys of the other head included), and it keeps
 // only its half of the output.  Decided from the call's shapes alone, so a
 // plan and the run that consumes it agree; decode calls only (no qo_indptr),
 // and batches of at least kPairMinBatch requests, whose items are long enough

@@ -478,7 +478,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
     const float l_tot = rows4_sum(l_run[rg]);
-    const float inv = l_tot > 0.f ? vscale / l_tot : 0.f;
+    const float inv = l_tot > 0.f ? vscale / l_tot : (l_tot == 0.f ? 0.f : __builtin_nanf(""));  // NaN: row stays NaN
     const int n = row0 + WROWS * wave + 16 * rg + col;
     if (n >= rows_total) continue;
     const int tok = n / G, g = n - tok * G;
