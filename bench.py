@@ -884,6 +884,44 @@ def _prefill_split(w, q, layer, events):
     return out
 
 
+def side_configs(args, dev) -> dict:
+    """The other BASELINE configs at full size, compact, for the default run:
+    c5 (fp8 KV decode) and c2 (Orpheus decode) as decode-kernel GB/s and
+    fraction of HBM peak, c4 (BAGEL ragged prefill + decode) as prefill-kernel
+    MFMA fraction plus its short-query decode part.  Each is the same
+    measurement as ``--config cN`` (fewer steps, no side measurements), run
+    after the headline config's buffers are freed."""
+    out = {}
+    for name in ("c5", "c2", "c4"):
+        sub = argparse.Namespace(**vars(args))
+        sub.config, sub.steps, sub.warmup = name, min(args.steps, 10), min(args.warmup, 3)
+        sub.no_extra, sub.no_cpu_baseline = True, True
+        torch.cuda.empty_cache()
+        if S.SPECS[name].prefill_chunks:
+            r = bench_prefill(sub, dev)
+            rf = r["roofline"]
+            sq = rf["short_query_part"]
+            out[name] = {
+                "workload": r["config"]["workload"], "steps": sub.steps, "ms_per_step": r["ms_per_step"],
+                "tokens_per_s": r["value"],
+                "prefill_kernel": rf["kernel"], "prefill_kernel_us": rf["kernel_us"],
+                "algorithmic_flops": rf["algorithmic_flops"], "TFLOPs": rf["achieved"],
+                "mfma_frac": rf["frac"], "short_query_us": sq["us"], "short_query_bytes": sq["algorithmic_bytes"],
+                "short_query_GBps": sq["GBps"], "short_query_hbm_frac": sq["GBps"] / HBM_PEAK_GBS,
+            }
+        else:
+            r = bench_decode(sub, dev)
+            rf = r["roofline"]
+            out[name] = {
+                "workload": r["config"]["workload"], "batch": r["config"]["batch"], "kv_dtype": r["config"]["kv_dtype"],
+                "steps": sub.steps, "ms_per_step": r["ms_per_step"], "tokens_per_s": r["value"],
+                "kernel": rf["kernel"], "kernel_us": rf["kernel_us"], "decode_plus_merge_us": rf["decode_plus_merge_us"],
+                "algorithmic_bytes": rf["algorithmic_bytes"], "GBps": rf["achieved"], "hbm_frac": rf["frac"],
+            }
+        _log(f"{name}: " + json.dumps({k: v for k, v in out[name].items() if k != "workload"}))
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -894,6 +932,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true",
                     help="only the step loop: skip the side measurements (RoPE, KV transfer, "
                          "head_dim 256 and fp8-pool prefill), e.g. for counter runs")
+    ap.add_argument("--no-side-configs", action="store_true",
+                    help="c3: skip the compact c5 / c2 / c4 measurements that follow the headline")
     ap.add_argument("--trace-ranges", action="store_true",
                     help="decode configs: the manager pushes its tracing ranges (enable_nvtx), for rocprofv3 --marker-trace")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -913,6 +953,8 @@ def main() -> int:
         res = bench_prefill(args, dev)
     else:
         res = bench_decode(args, dev)
+    if args.config == "c3" and not args.no_extra and not args.no_side_configs:
+        res["configs"] = side_configs(args, dev)
     print(json.dumps(res), flush=True)
     return 0
 

@@ -13,8 +13,13 @@
  *   [max_pages, 2 (K,V), page_size, num_kv_heads, head_dim]
  * described by mi_paged_kv with explicit element strides.
  *
- * Threading: no global mutable state; plan and run of different workspaces
- * may run concurrently on different streams.
+ * Threading: plan and run of different workspaces may run concurrently on
+ * different streams.  Library-wide state: a per-device cache of the CU count
+ * (written once per device on first use; it feeds the split-KV partition of
+ * small decode jobs) and, for mi_decode_noalloc only, one static device
+ * scratch array per GPU with its address cached per device (see that entry
+ * point: calls that overlap on one GPU race there).  Everything else a call
+ * uses comes in through its arguments.
  */
 #ifndef MSTAR_AMD_H
 #define MSTAR_AMD_H

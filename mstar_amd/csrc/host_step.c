@@ -25,11 +25,23 @@ static PyObject *k_seq_len, *k_pos, *k_pages, *k_slot, *k_dev_list, *k_dev_len, 
 /* The instance dict is read directly on CPython 3.10 (the interpreter this
  * package builds for); later versions keep instance attributes in their own
  * layout, so there the generic attribute protocol is used. */
+#ifndef MI_DIRECT_DICT /* -DMI_DIRECT_DICT=0 builds the generic branch on any version (tested that way) */
 #if PY_VERSION_HEX < 0x030B0000
 #define MI_DIRECT_DICT 1
 #else
 #define MI_DIRECT_DICT 0
 #endif
+#endif
+
+/* Module name: _host_step, or another name given with -DMI_HOST_STEP_MODULE
+ * (the generic-attribute test build is loaded beside the default one). */
+#ifndef MI_HOST_STEP_MODULE
+#define MI_HOST_STEP_MODULE _host_step
+#endif
+#define MI_STR_(x) #x
+#define MI_STR(x) MI_STR_(x)
+#define MI_CAT_(a, b) a##b
+#define MI_CAT(a, b) MI_CAT_(a, b)
 
 /* New reference to attribute `k` of `o`, or NULL with an exception set. */
 static PyObject* get_attr(PyObject* o, PyObject* k) {
@@ -400,9 +412,10 @@ static PyMethodDef methods[] = {
     {NULL, NULL, 0, NULL},
 };
 
-static struct PyModuleDef module = {PyModuleDef_HEAD_INIT, "_host_step", NULL, -1, methods, NULL, NULL, NULL, NULL};
+static struct PyModuleDef module = {PyModuleDef_HEAD_INIT, MI_STR(MI_HOST_STEP_MODULE), NULL, -1, methods, NULL, NULL,
+                                     NULL, NULL};
 
-PyMODINIT_FUNC PyInit__host_step(void) {
+PyMODINIT_FUNC MI_CAT(PyInit_, MI_HOST_STEP_MODULE)(void) {
   k_seq_len = PyUnicode_InternFromString("seq_len");
   k_pos = PyUnicode_InternFromString("position_id_start");
   k_pages = PyUnicode_InternFromString("page_indices");

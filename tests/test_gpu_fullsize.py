@@ -16,8 +16,10 @@ allocation, block-table delta, ``mi_pack_plan``), ``set_kv_cache``, ``run``
   fp32 attention computed on the GPU (gathered pages, GQA by
   ``repeat_interleave``) over the same cache after the append.
 
-At B=256 the split-KV items of c3 and c5 span about 409 and 585 pages, so
-every decode wavefront walks two or three 64-page windows of page ids.
+At B=256 the split-KV items of c3 (a plan over kv-head pairs: a quarter as
+many items per head as a per-head plan) and c5 span several hundred pages
+(the test logs the count and requires more than 256), so every decode
+wavefront walks two or more 64-page windows of page ids.
 """
 
 import math

@@ -2,7 +2,13 @@
 replaces: PagedAllocationManager.alloc_batch + DeviceBlockTable.prepare_meta
 (the pack kernel's metadata) and advance_seq_lens, on identical managers driven
 through the same random step sequences (decode steps, prefill chunks, lists
-replaced or edited in place, new and removed requests, a pool that runs dry)."""
+replaced or edited in place, new and removed requests, a pool that runs dry).
+
+Every test runs on both builds of the extension: the default one (on this
+CPython 3.10 it reads instance dicts directly) and ``_host_step_generic``,
+compiled with ``MI_DIRECT_DICT=0``: the generic attribute protocol that
+CPython 3.11 and later compile (the reference targets 3.12)."""
+import importlib
 import random
 
 import numpy as np
@@ -11,8 +17,24 @@ import pytest
 from mstar_amd import kv_store
 from mstar_amd.kv_store import AllocationFailedError, KVCacheConfig, PagedAllocationManager
 
-hs = kv_store._host_step
-pytestmark = pytest.mark.skipif(hs is None, reason="host_step extension not built (mstar_amd.build.build_host)")
+
+def _load(name):
+    try:
+        return importlib.import_module(f"mstar_amd.{name}")
+    except ImportError:
+        return None
+
+
+BUILDS = {name: _load(name) for name in ("_host_step", "_host_step_generic")}
+
+
+@pytest.fixture(params=list(BUILDS))
+def hs(request, monkeypatch):
+    mod = BUILDS[request.param]
+    if mod is None:
+        pytest.skip(f"{request.param} not built (mstar_amd.build.build_host)")
+    monkeypatch.setattr(kv_store, "_host_step", mod)
+    return mod
 
 
 def _mgr(pages: int) -> PagedAllocationManager:
@@ -48,7 +70,7 @@ def _advance_py(states, seq_lens, adv):
 
 
 @pytest.mark.parametrize("seed", range(6))
-def test_host_step_matches_python_loops(seed):
+def test_host_step_matches_python_loops(seed, hs):
     rng = random.Random(seed)
     a, b = _mgr(600), _mgr(600)
     rids = []
@@ -112,7 +134,7 @@ def test_host_step_matches_python_loops(seed):
         assert _snapshot(a) == _snapshot(b), step
 
 
-def test_host_step_matches_python_loops_at_large_batch():
+def test_host_step_matches_python_loops_at_large_batch(hs):
     a, b = _mgr(40000), _mgr(40000)
     rng = random.Random(9)
     rids = [f"r{i}" for i in range(1100)]
@@ -132,7 +154,7 @@ def test_host_step_matches_python_loops_at_large_batch():
         assert _snapshot(a) == _snapshot(b)
 
 
-def test_host_step_accepts_numpy_lengths():
+def test_host_step_accepts_numpy_lengths(hs):
     a, b = _mgr(64), _mgr(64)
     for m in (a, b):
         for r in ("x", "y"):
@@ -146,7 +168,7 @@ def test_host_step_accepts_numpy_lengths():
     assert [b.get_state(r, "main").seq_len for r in ("x", "y")] == [17, 3]
 
 
-def test_host_step_rejects_rows_longer_than_the_table():
+def test_host_step_rejects_rows_longer_than_the_table(hs):
     m = _mgr(600)
     m.add_request("x", ["main"])
     st = m.get_state("x", "main")
@@ -155,7 +177,23 @@ def test_host_step_rejects_rows_longer_than_the_table():
         m.alloc_pack_meta([("x", "main")], [st], [0], m.state_generation)
 
 
-def test_host_step_needs_counts_pages():
+def test_generic_build_uses_attribute_protocol():
+    """The generic build reads and writes state attributes through
+    getattr/setattr, so it also works on objects without an instance dict."""
+    gen = BUILDS["_host_step_generic"]
+    if gen is None:
+        pytest.skip("_host_step_generic not built")
+
+    class Slotted:
+        __slots__ = ("seq_len", "position_id_start", "page_indices")
+
+    st = Slotted()
+    st.seq_len, st.position_id_start, st.page_indices = 5, 2, [1]
+    gen.advance([st], [3], None)
+    assert (st.seq_len, st.position_id_start) == (8, 5)
+
+
+def test_host_step_needs_counts_pages(hs):
     m = _mgr(64)
     m.add_request("x", ["main"])
     st = m.get_state("x", "main")

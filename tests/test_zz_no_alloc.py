@@ -94,6 +94,25 @@ def test_noalloc_matches_workspace_path_twice(gpu):
         assert err < 2e-2
 
 
+def test_noalloc_paired_plan_twice(gpu):
+    """Batches of >= 128 requests at head_dim 128 with <= 8 q-heads per kv-head
+    plan and run over kv-head pairs (a head_dim 256 plan over half the heads)
+    through the same static scratch; two calls in a row, the second smaller,
+    each bit-identical to the two-call path and within 2e-2 of the oracle."""
+    rng = np.random.default_rng(12)
+    for b, seed in ((160, 21), (128, 22)):
+        lens = rng.integers(1, 900, b).tolist()
+        lens[:2] = [9000, 4100]  # split requests: partials and merge in the scratch
+        pool = int(sum(-(-np.array(lens) // 16))) + 16
+        log(f"noalloc paired decode B={b}")
+        outs, locs, ref, _ = _both(gpu, lens, None, 32, 4, 128, 16, pool, seed, 0)
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), "outputs differ from the two-call path"
+        assert torch.equal(locs[0], locs[1])
+        err = max_abs(outs[1], ref)
+        log(f"  max_abs vs oracle {err:.3e}")
+        assert err < 2e-2
+
+
 def test_noalloc_short_query_ragged(gpu):
     # two query tokens per request (qo_len * group = 16 rows), causal
     lens, new = [40, 3000, 17, 16], [2, 2, 2, 1]
