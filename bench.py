@@ -653,19 +653,26 @@ def bench_decode_side(dev, steps: int) -> dict:
     }
 
 
+def short_rows(bt) -> int:
+    """The library's short-query threshold (rows per request) for this batch's shape."""
+    s = bt.spec
+    return _lib.lib().mi_prefill_short_rows(len(bt.kv_len), s.num_qo_heads, s.num_kv_heads, s.head_dim)
+
+
 def prefill_flops(bt) -> tuple[int, int]:
     """(flops of the MFMA-tile requests, flops of the short-query requests) of one causal step.
 
     4*D*Hq flops per visible (query, key) pair: q.k and p.v, a multiply-add each.
-    Requests with qo_len*G <= 16 rows run on the decode kernel.
+    Requests with qo_len*G at most ``mi_prefill_short_rows`` rows run on the decode kernel.
     """
     s = bt.spec
     g = s.num_qo_heads // s.num_kv_heads
+    short = short_rows(bt)
     long_f = short_f = 0
     for kvl, qo in zip(bt.kv_len.tolist(), bt.new_len.tolist()):
         pairs = qo * (kvl - qo) + qo * (qo + 1) // 2
         f = 4 * s.head_dim * s.num_qo_heads * pairs
-        if qo * g > 16:
+        if qo * g > short:
             long_f += f
         else:
             short_f += f
@@ -720,8 +727,9 @@ def bench_prefill(args, dev) -> dict:
     achieved = long_f / tile_s / 1e12
     short_bytes = 0
     g_ = s.num_qo_heads // s.num_kv_heads
+    short = short_rows(bt)
     for kvl, qo in zip(bt.kv_len.tolist(), bt.new_len.tolist()):
-        if qo * g_ <= 16:
+        if qo * g_ <= short:
             short_bytes += kvl * s.num_kv_heads * s.head_dim * 2 * 2 + qo * s.num_qo_heads * s.head_dim * 2 * 2
     res = {
         "metric": "ragged prefill+decode attn tokens/s + prefill MFMA TFLOP/s, 1 MI355X",

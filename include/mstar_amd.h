@@ -45,7 +45,7 @@ extern "C" {
 #define MI_ERR_WORKSPACE (-3)   /* workspace too small or not planned for this call */
 #define MI_ERR_LAUNCH (-4)      /* HIP launch error */
 
-#define MI_ABI_VERSION 2
+#define MI_ABI_VERSION 3
 
 /* One layer of the paged KV cache. Strides are in elements. */
 typedef struct mi_paged_kv {
@@ -253,8 +253,9 @@ int mi_kv_append(const mi_paged_kv* kv, const void* k, const void* v, int32_t sr
  * for t < qo_indptr[batch] (entries in [qo_indptr[batch], token_map_len) are set
  * to 0, like the graph-mode tail fill of flashinfer_utils.py:251-253), and the
  * work partition for mi_prefill_run into the workspace.  Requests whose
- * qo_len * (num_qo_heads/num_kv_heads) <= 16 go to the split-KV decode kernel,
- * longer ones to the MFMA prefill kernel.
+ * qo_len * (num_qo_heads/num_kv_heads) <= mi_prefill_short_rows(...) (16, or 8
+ * for a plan over kv-head pairs) go to the split-KV decode kernel, longer
+ * ones to the MFMA prefill kernel.
  * max_qo_tokens bounds qo_indptr[batch] (grid sizing without a host sync);
  * mi_prefill_run must get the same batch, max_qo_tokens and workspace.
  * mi_prefill_run replaces FlashInferPrefillWrapper.run (:258-269):
@@ -271,6 +272,15 @@ int mi_kv_append(const mi_paged_kv* kv, const void* k, const void* v, int32_t sr
  * ------------------------------------------------------------------------ */
 int64_t mi_prefill_workspace_bytes(int32_t batch, int32_t max_qo_tokens, int32_t num_qo_heads,
                                    int32_t num_kv_heads, int32_t head_dim);
+/* Which requests of a plan of this shape are short-query requests (run by
+ * mi_prefill_short): those with qo_len * (num_qo_heads / num_kv_heads) at most
+ * the returned number of rows; the others are mi_prefill_tiles' work.  16, or
+ * 8 when the plan reads kv-head pairs as one row (batch >= 128, head_dim 128,
+ * at most 8 q-heads per kv-head, an even number of kv-heads).  For a caller
+ * that skips a launch with no work; negative on invalid arguments.  Helper
+ * of this library's split of FlashInferPrefillWrapper.run, no counterpart in
+ * the reference. */
+int32_t mi_prefill_short_rows(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim);
 int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
                     const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
                     int32_t max_qo_tokens, int32_t page_size, int32_t num_qo_heads,

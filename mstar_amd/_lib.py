@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_PATH = Path(__file__).resolve().parent / "libmstar_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # dtype codes (mstar_amd.h)
 MI_BF16 = 0
@@ -117,6 +117,7 @@ SIGNATURES = {
         [ctypes.POINTER(MiPagedKV), _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _P, _I64, _I32, _P, _P],
     ),
     "mi_prefill_workspace_bytes": (_I64, [_I32, _I32, _I32, _I32, _I32]),
+    "mi_prefill_short_rows": (_I32, [_I32, _I32, _I32, _I32]),
     "mi_prefill_plan": (
         ctypes.c_int,
         [_P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _P, _I32, _P, _I64, _P],

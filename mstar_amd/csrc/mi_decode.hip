@@ -512,7 +512,7 @@ __global__ __launch_bounds__(256) void merge_kernel(DecodeParams p, int32_t batc
   }
   const int G = p.group;
   const int rows = (PAIR ? 2 : 1) * qo_len * G;
-  if (rows > kRows) return;  // long-query request: written by the prefill kernel
+  if (qo_len * G > p.short_rows) return;  // long-query request: written by the prefill kernel
   const int lane = lane_id();
   const int wave = (int)threadIdx.x >> 6;
   const int col = lane & 15, grp = lane >> 4;
@@ -608,7 +608,7 @@ int decode_plan_params(const int32_t* qo_indptr, const int32_t* kv_indptr, const
                        const int32_t* last_page_len, int32_t batch, int32_t page_size,
                        int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                        int64_t* kv_locations, void* workspace, int64_t workspace_bytes,
-                       int64_t ws_offset, PlanParams* out) {
+                       int64_t ws_offset, PlanParams* out, bool ragged_pair) {
   if (batch < 0 || !kv_indptr || !last_page_len || !workspace) return MI_ERR_INVALID;
   if (batch > 0 && !kv_indices) return MI_ERR_INVALID;
   if (num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads) return MI_ERR_INVALID;
@@ -616,11 +616,12 @@ int decode_plan_params(const int32_t* qo_indptr, const int32_t* kv_indptr, const
   if (page_size <= 0) return MI_ERR_INVALID;
   if (page_size % 16) return MI_ERR_UNSUPPORTED;
   if (!supported_head_dim(head_dim)) return MI_ERR_UNSUPPORTED;
-  const bool pair = pair_heads(qo_indptr, batch, num_kv_heads, num_qo_heads / num_kv_heads, head_dim);
+  const bool pair = pair_heads(qo_indptr, batch, num_kv_heads, num_qo_heads / num_kv_heads, head_dim, ragged_pair);
   const SplitLayout L = split_layout(batch, num_kv_heads, head_dim, workspace_bytes - ws_offset, pair);
   if (L.max_chunks <= batch || workspace_bytes < ws_offset + L.total) return MI_ERR_WORKSPACE;
   uint8_t* ws = (uint8_t*)workspace + ws_offset;
   PlanParams& pp = *out;
+  pp.short_rows = pair_short_rows(pair);
   pp.qo_indptr = qo_indptr;
   pp.kv_indptr = kv_indptr;
   pp.num_pages = nullptr;
@@ -712,7 +713,8 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
                     const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
                     int32_t num_qo_heads, int32_t causal, float sm_scale, void* workspace,
                     int64_t workspace_bytes, int64_t ws_offset, void* out,
-                    int64_t out_stride_token, int64_t out_stride_head, int phases, hipStream_t stream) {
+                    int64_t out_stride_token, int64_t out_stride_head, int phases, hipStream_t stream,
+                    bool ragged_pair) {
   if (!kv || batch < 0 || !workspace) return MI_ERR_INVALID;
   if (batch == 0) return MI_OK;
   if (!q || !out || !kv->data || !kv_indptr || !kv_indices || !last_page_len) return MI_ERR_INVALID;
@@ -731,7 +733,7 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
       !rows_aligned16(out, out_stride_token, out_stride_head, qesz) || !kv_aligned16(kv))
     return MI_ERR_INVALID;
   // the same pairing decision as the plan's (shapes only), so the layouts agree
-  const bool pair = pair_heads(qo_indptr, batch, nkv, num_qo_heads / nkv, D);
+  const bool pair = pair_heads(qo_indptr, batch, nkv, num_qo_heads / nkv, D, ragged_pair);
   const SplitLayout L = split_layout(batch, nkv, D, workspace_bytes - ws_offset, pair);
   if (L.max_chunks <= batch || workspace_bytes < ws_offset + L.total) return MI_ERR_WORKSPACE;
   uint8_t* ws = (uint8_t*)workspace + ws_offset;
@@ -768,6 +770,7 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
   dp.page_size = kv->page_size;
   dp.causal = causal ? 1 : 0;
   dp.scale_log2 = sm_scale * 1.4426950408889634f;
+  dp.short_rows = pair_short_rows(pair);
   const int grid = (int)((L.max_chunks + 7) / 8 * 8 * (int64_t)nkv);
   int st;
   if (pair_kernel) {

@@ -28,12 +28,22 @@ SplitLayout split_layout(int32_t batch, int32_t nkv, int32_t head_dim, int64_t w
 // for the one-workgroup-per-CU head_dim 256 kernel (c3, B=256: 542 -> 515 us;
 // c2, B=64, min-chunk items: 57 -> 60 us).  The run uses the paired kernel
 // for 16-bit caches only (fp8 pairs are 256-byte rows: c5 400 -> 410 us).
+// A ragged batch (qo_indptr given) pairs only on the prefill path (`ragged`),
+// where a request that does not fit a paired row block has somewhere else to
+// go: there the short-query threshold halves (pair_short_rows) and the MFMA
+// tiles take the requests between the two thresholds.
 constexpr int32_t kPairMinBatch = 128;
 inline bool pair_heads(const int32_t* qo_indptr, int32_t batch, int32_t num_kv_heads, int32_t group,
-                       int32_t head_dim) {
-  return !qo_indptr && batch >= kPairMinBatch && head_dim == 128 && num_kv_heads % 2 == 0 && group >= 1 &&
-         2 * group <= 16;
+                       int32_t head_dim, bool ragged = false) {
+  return (!qo_indptr || ragged) && batch >= kPairMinBatch && head_dim == 128 && num_kv_heads % 2 == 0 &&
+         group >= 1 && 2 * group <= 16;
 }
+// Short-query requests of a ragged batch (qo_len * group <= this many rows)
+// run on the split-KV decode kernels, longer ones on the MFMA prefill tiles.
+// 16 rows (one MFMA column block); 8 for a paired plan, whose column block
+// holds a request's rows of both heads of a pair.
+constexpr int32_t kShortRowsMax = 16;
+inline int32_t pair_short_rows(bool pair) { return pair ? kShortRowsMax / 2 : kShortRowsMax; }
 
 int decode_plan_impl(const int32_t* qo_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
                      const int32_t* last_page_len, int32_t batch, int32_t page_size,
@@ -47,7 +57,7 @@ int decode_plan_params(const int32_t* qo_indptr, const int32_t* kv_indptr, const
                        const int32_t* last_page_len, int32_t batch, int32_t page_size,
                        int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                        int64_t* kv_locations, void* workspace, int64_t workspace_bytes,
-                       int64_t ws_offset, PlanParams* out);
+                       int64_t ws_offset, PlanParams* out, bool ragged_pair = false);
 
 enum : int { kPhaseAttend = 1, kPhaseMerge = 2 };
 
@@ -86,6 +96,7 @@ struct DecodeParams {
   int64_t out_stride_tok, out_stride_head;
   int32_t num_kv_heads, group, page_size, causal;
   float scale_log2;
+  int32_t short_rows = kShortRowsMax;  // ragged batches: requests with qo_len * group above this are not ours
 };
 
 // fp32 KV (q, cache and output in fp32): the attend phase of a split-KV plan
@@ -102,7 +113,8 @@ int decode_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_token, int6
                     const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
                     int32_t num_qo_heads, int32_t causal, float sm_scale, void* workspace,
                     int64_t workspace_bytes, int64_t ws_offset, void* out,
-                    int64_t out_stride_token, int64_t out_stride_head, int phases, hipStream_t stream);
+                    int64_t out_stride_token, int64_t out_stride_head, int phases, hipStream_t stream,
+                    bool ragged_pair = false);
 
 // Exclusive prefix sum over a 1024-thread block; `smem` holds >= 16 ints.
 __device__ __forceinline__ int block_exclusive_scan_1024(int v, int& total, int* smem) {

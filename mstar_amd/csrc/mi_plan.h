@@ -37,6 +37,7 @@ struct PlanParams {
   const int32_t* last_page_len;
   int32_t batch, target, min_chunk_pages, max_chunks, group;
   int32_t slots, floor_pages;  // small jobs: items of down to floor_pages while at most `slots` items
+  int32_t short_rows = kShortRowsMax;  // ragged batch: requests with qo_len * group <= short_rows
   int32_t* hdr;
   int32_t* chunk_indptr;
   int4* work;
@@ -76,7 +77,7 @@ __device__ inline void decode_plan_body(const PlanParams& p) {
     int n = np > 0 ? (np + c - 1) / c : 0;
     if (p.qo_indptr) {  // ragged batch: only short-query requests belong to this kernel
       const int qo_len = p.qo_indptr[b + 1] - p.qo_indptr[b];
-      if (qo_len <= 0 || qo_len * p.group > kRows) n = 0;
+      if (qo_len <= 0 || qo_len * p.group > p.short_rows) n = 0;
     }
     return n;
   };

@@ -30,7 +30,7 @@
 #include "mi_prefill_kernel.h"
 
 namespace mi {
-constexpr int kShortRows = 16;  // qo_len * group <= 16 -> decode kernel
+constexpr int kShortRows = kShortRowsMax;  // qo_len * group <= 16 -> decode kernel (8 on a paired plan)
 
 // Workspace: header | per-XCD queue counters + finished-workgroup counter |
 // tile list | tile cost prefix | unit order | decode split plan.
@@ -124,6 +124,7 @@ struct PfPlanArgs {
   const int32_t* kv_indptr;
   const int32_t* last_page_len;
   int32_t batch, page_size, group, nkv, tile_rows, max_tiles, causal;
+  int32_t short_rows;  // requests with qo_len * group <= short_rows are the decode plan's, not tiles
   int32_t* hdr;
   int2* tiles;
   int32_t* tcum;
@@ -151,7 +152,7 @@ __device__ inline void prefill_plan_body(const PfPlanArgs& a) {
     if (b < a.batch) {
       const int qo_len = a.qo_indptr[b + 1] - a.qo_indptr[b];
       const int rows = qo_len * group;
-      n = rows > kShortRows ? (rows + tile_rows - 1) / tile_rows : 0;
+      n = rows > a.short_rows ? (rows + tile_rows - 1) / tile_rows : 0;
       s_qol[tid] = qo_len;
       s_kvl[tid] = (a.kv_indptr[b + 1] - a.kv_indptr[b] - 1) * a.page_size + a.last_page_len[b];
     }
@@ -289,6 +290,14 @@ extern "C" int64_t mi_prefill_workspace_bytes(int32_t batch, int32_t max_qo_toke
   return L.split + split_layout(batch, num_kv_heads, head_dim, -1).total;
 }
 
+extern "C" int32_t mi_prefill_short_rows(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                         int32_t head_dim) {
+  using namespace mi;
+  if (batch < 0 || num_kv_heads <= 0 || num_qo_heads <= 0 || num_qo_heads % num_kv_heads) return MI_ERR_INVALID;
+  const int32_t G = num_qo_heads / num_kv_heads;
+  return pair_short_rows(pair_heads(nullptr, batch, num_kv_heads, G, head_dim, true));
+}
+
 extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indptr,
                                const int32_t* kv_indices, const int32_t* last_page_len, int32_t batch,
                                int32_t max_qo_tokens, int32_t page_size, int32_t num_qo_heads,
@@ -309,7 +318,7 @@ extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
   uint8_t* ws = (uint8_t*)workspace;
   PlanParams d{};
   const int st = decode_plan_params(qo_indptr, kv_indptr, kv_indices, last_page_len, batch, page_size, num_qo_heads,
-                                    num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, L.split, &d);
+                                    num_kv_heads, head_dim, nullptr, workspace, workspace_bytes, L.split, &d, true);
   if (st != MI_OK) return st;
   PfPlanArgs a;
   a.qo_indptr = qo_indptr;
@@ -322,6 +331,7 @@ extern "C" int mi_prefill_plan(const int32_t* qo_indptr, const int32_t* kv_indpt
   a.tile_rows = pf_rows(head_dim);
   a.max_tiles = L.max_tiles;
   a.causal = 1;  // cost model: causal
+  a.short_rows = d.short_rows;  // the decode plan's threshold: every request goes to exactly one of the two
   a.hdr = (int32_t*)(ws + L.hdr);
   a.tiles = (int2*)(ws + L.tiles);
   a.tcum = (int32_t*)(ws + L.tcum);
@@ -383,7 +393,7 @@ static int prefill_run_impl(const void* q, int32_t q_dtype, int64_t q_stride_tok
   if (phases & kPhaseShort) {
     st = decode_run_impl(q, q_dtype, q_stride_token, q_stride_head, kv, qo_indptr, kv_indptr, kv_indices,
                          last_page_len, batch, num_qo_heads, causal, sm_scale, workspace, workspace_bytes,
-                         L.split, out, out_stride_token, out_stride_head, kPhaseAttend | kPhaseMerge, s);
+                         L.split, out, out_stride_token, out_stride_head, kPhaseAttend | kPhaseMerge, s, true);
     if (st != MI_OK) return st;
   }
   if (!(phases & kPhaseTiles)) return MI_OK;

@@ -42,10 +42,6 @@ __all__ = [
 ]
 
 _MAX_GROUP = 16  # q heads per kv head handled by one MFMA tile
-# A prefill request of at most this many (token, q-head) rows goes to the
-# split-KV decode kernel (mi_prefill_short), a longer one to the MFMA tiles
-# (mi_prefill_tiles); kShortRows in mi_prefill.hip.
-_SHORT_ROWS = 16
 
 
 def _check_heads(num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int) -> None:
@@ -515,9 +511,12 @@ class PagedPrefillWrapper(_FusedRopeAppend):
         # later mix, device inputs are not read back) both are launched, and
         # a launch without work exits at once.
         if on_cpu and not self.use_cuda_graph:
+            # a request of at most `short` (token, q-head) rows goes to the split-KV
+            # decode kernel (mi_prefill_short), a longer one to the MFMA tiles
+            short = _lib.lib().mi_prefill_short_rows(n_req, self.num_qo_heads, self.num_kv_heads, self.head_dim)
             rows = torch.diff(qo_indptr.to(torch.int64)) * (self.num_qo_heads // self.num_kv_heads)
-            self._run_short = bool(((rows > 0) & (rows <= _SHORT_ROWS)).any())
-            self._run_tiles = bool((rows > _SHORT_ROWS).any())
+            self._run_short = bool(((rows > 0) & (rows <= short)).any())
+            self._run_tiles = bool((rows > short).any())
         else:
             self._run_short = self._run_tiles = True
 

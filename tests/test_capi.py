@@ -72,6 +72,17 @@ def test_workspace_sizes_are_host_arithmetic(L):
     assert L.mi_prefill_workspace_bytes(8, 4096, 32, 5, 128) < 0  # 32 % 5 != 0
 
 
+def test_prefill_short_rows(L):
+    """Short-query threshold: 16 rows, 8 on plans that read kv-head pairs
+    (batch >= 128, head_dim 128, group <= 8, even kv-head count)."""
+    assert L.mi_prefill_short_rows(8, 28, 4, 128) == 16      # batch below 128
+    assert L.mi_prefill_short_rows(128, 28, 4, 128) == 8     # c4's shape: paired
+    assert L.mi_prefill_short_rows(200, 32, 4, 256) == 16    # head_dim 256
+    assert L.mi_prefill_short_rows(200, 36, 4, 128) == 16    # group 9: a pair's rows exceed 16
+    assert L.mi_prefill_short_rows(200, 24, 3, 128) == 16    # odd kv-head count
+    assert L.mi_prefill_short_rows(200, 30, 4, 128) < 0      # heads not a multiple
+
+
 def test_invalid_arguments_are_rejected_before_launch(L):
     nul = None
     # negative batch, null outputs

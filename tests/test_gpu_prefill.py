@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from gpu_helpers import A, P, S, custom_batch, log, max_abs, random_cache, workspace
+from mstar_amd import _lib
 from mstar_amd.paged_attention import FlashInferPrefillWrapper
 
 pytestmark = pytest.mark.gpu
@@ -116,6 +117,43 @@ def test_prefill_ragged_mix(gpu, causal, hq, hkv, d, ps):
     err = max_abs(out, ref)
     log(f"  max_abs={err:.3e}")
     assert err < TOL
+
+
+def _paired_mix(seed, b=140):
+    """A ragged batch of >= 128 requests at head_dim 128 (its short part reads
+    kv-head pairs): single-token requests (paired decode), two- and
+    three-token requests whose 14-21 rows no longer fit a paired column block
+    (MFMA tiles), empty requests and two long chunks."""
+    rng = np.random.default_rng(seed)
+    kv = rng.integers(2, 600, b)
+    new = np.ones(b, dtype=np.int64)
+    new[5:9] = [2, 3, 2, 0]
+    kv[10:12] = [900, 700]
+    new[10:12] = [300, 640]
+    kv[20] = 5000  # a long single-token request: split items and a merge
+    return kv.tolist(), new.tolist()
+
+
+@pytest.mark.parametrize("dtype,fp8", [(torch.bfloat16, False), (torch.float16, False), (torch.bfloat16, True),
+                                       (torch.float32, False)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_paired_short_queries(gpu, dtype, fp8, causal):
+    """Short-query requests of a large ragged batch run on the paired kernel
+    (bf16/fp16; fp8 and fp32 run the per-head kernels on the paired plan)."""
+    kv, new = _paired_mix(7)
+    assert _lib.lib().mi_prefill_short_rows(len(kv), 28, 4, 128) == 8
+    out, ref = _run_prefill(gpu, 28, 4, 128, 16, kv, new, causal, seed=23, fp8=fp8, dtype=dtype)
+    err = max_abs(out, ref)
+    log(f"paired short queries {dtype} fp8={fp8} causal={causal}: max_abs={err:.3e}")
+    assert err < (TOL_FP8 if fp8 else (2e-5 if dtype == torch.float32 else TOL))
+
+
+def test_prefill_paired_short_queries_only(gpu):
+    """Every request single-token: run() launches only the short half, paired."""
+    rng = np.random.default_rng(3)
+    kv = rng.integers(1, 900, 130).tolist()
+    out, ref = _run_prefill(gpu, 32, 4, 128, 16, kv, [1] * 130, True, seed=29)
+    assert max_abs(out, ref) < TOL
 
 
 @pytest.mark.parametrize("kv_lens,new_lens,launches", [([40, 300, 17, 260], [1, 2, 0, 1], "short"),
@@ -232,10 +270,12 @@ def test_prefill_plan_tiles_costs_and_queues(gpu):
            causal=True)
     torch.cuda.synchronize()
     # host listing: tiles of 256 rows, request order, last rows first; cost = 32-key steps to the causal limit
+    short = _lib.lib().mi_prefill_short_rows(b, hq, hkv, d)
+    assert short == 8  # 1500 requests, head_dim 128, 7 q-heads per kv-head: the short part reads kv-head pairs
     exp_tiles, exp_cost = [], []
     for r in range(b):
         rows = int(new[r]) * g_
-        if rows <= 16:
+        if rows <= short:
             continue
         n = -(-rows // 256)
         for i in range(n):
