@@ -207,14 +207,16 @@ def _run_split(w, q, kv_layer, ks, vs, events):
     return out
 
 
-def decode_graph_us(cm, q, steps: int, per_layer: int = 4) -> tuple[float, float]:
+def decode_graph_us(cm, q, steps: int, per_graph: int = 12) -> tuple[float, float]:
     """(decode kernel us, decode + merge us) per launch of the current plan, from
-    HIP graph replays: ``per_layer`` launches on every layer of the pool, in
-    turn, captured into one graph; HIP events around each replay on the
-    launch stream.  Replays time the GPU alone, without the host issue gaps
-    that sit between a short kernel and the events around it."""
+    HIP graph replays: at least ``per_graph`` launches (the same number on every
+    layer of the pool, in turn) captured into one graph; HIP events around each
+    replay on the launch stream.  Replays time the GPU alone, without the host
+    issue gaps that sit between a short kernel and the events around it; the
+    graph launch itself is spread over the launches of one replay."""
     w = cm._plan_states["main"].wrapper
     layers = cm.kv_cache.shape[0]
+    per_layer = -(-per_graph // layers)
     out = torch.empty_like(q)
     argv = [_decode_args(w, q, cm.kv_cache[i], *_layer_scales(cm, i), out) for i in range(layers)]
     L = _lib.lib()
@@ -415,7 +417,7 @@ def bench_decode(args, dev) -> dict:
                                if traffic is not None else None),
             "kernel": "decode_kernel",
             "kernel_us": dec_us,
-            "kernel_us_how": (f"HIP graph replay of {4 * layers} decode launches of the last step's plan "
+            "kernel_us_how": (f"HIP graph replay of {-(-12 // layers) * layers} decode launches of the last step's plan "
                               f"({layers} pool layer(s) in turn), HIP events on the launch stream"),
             "algorithmic_bytes": graph_bytes,
             "decode_plus_merge_us": dm_us,
@@ -897,12 +899,12 @@ def side_configs(args, dev) -> dict:
     c5 (fp8 KV decode) and c2 (Orpheus decode) as decode-kernel GB/s and
     fraction of HBM peak, c4 (BAGEL ragged prefill + decode) as prefill-kernel
     MFMA fraction plus its short-query decode part.  Each is the same
-    measurement as ``--config cN`` (fewer steps, no side measurements), run
-    after the headline config's buffers are freed."""
+    measurement as ``--config cN`` (same steps and warm-up, no side
+    measurements), run after the headline config's buffers are freed."""
     out = {}
     for name in ("c5", "c2", "c4"):
         sub = argparse.Namespace(**vars(args))
-        sub.config, sub.steps, sub.warmup = name, min(args.steps, 10), min(args.warmup, 3)
+        sub.config = name
         sub.no_extra, sub.no_cpu_baseline = True, True
         torch.cuda.empty_cache()
         if S.SPECS[name].prefill_chunks:
