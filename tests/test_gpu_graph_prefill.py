@@ -31,10 +31,33 @@ from mstar_amd.paged_attention import FlashInferPrefillWrapper
 
 pytestmark = pytest.mark.gpu
 
-HQ, HKV, D, PS, LAYERS, BS, SEQ, POOL = 28, 4, 128, 16, 2, 4, 64, 512
+HQ, HKV, D, PS, LAYERS, SEQ = 28, 4, 128, 16, 2, 64
 
 
-def test_packed_prefill_graph_replays_with_padding(gpu):
+def _schedule(bs):
+    """(live requests, new tokens each) per replay."""
+    if bs == 4:
+        # chunks over growing prefixes, short (decode-kernel) queries, zero-length padding after the real requests
+        return [
+            (["r0", "r1", "r2"], [64, 10, 33]),
+            (["r0", "r1", "r2", "r3"], [5, 64, 17, 1]),
+            (["r1", "r3"], [2, 40]),
+            (["r0", "r2", "r3"], [1, 2, 64]),
+            (["r3"], [7]),
+        ]
+    # >= 128 slots: the short-query half reads kv-head pairs (one-token requests); two- and
+    # three-token requests (14-21 rows) and chunks go to the tiles
+    rng = np.random.default_rng(bs)
+    out = []
+    for n_live in (bs, bs - 3, 100, bs):
+        new = rng.choice([1, 1, 1, 1, 2, 3, 17, 64], n_live).tolist()
+        out.append(([f"r{i}" for i in range(n_live)], new))
+    return out
+
+
+@pytest.mark.parametrize("BS", [4, 130])
+def test_packed_prefill_graph_replays_with_padding(gpu, BS):
+    POOL = 512 if BS == 4 else 4096
     cfg = KVCacheConfig(num_layers=LAYERS, num_kv_heads=HKV, head_dim=D, max_seq_len=4096, max_num_pages=POOL,
                         page_size=PS, num_qo_heads=HQ)
     g = torch.Generator().manual_seed(11)
@@ -73,16 +96,10 @@ def test_packed_prefill_graph_replays_with_padding(gpu):
     real = [f"r{i}" for i in range(BS)]
     for r in real:
         mgr.add_request(r, ["main"])
-    # (real requests, new tokens each): chunks over growing prefixes, short (decode-kernel) queries,
-    # and zero-length padding after the real requests
-    schedule = [
-        (["r0", "r1", "r2"], [64, 10, 33]),
-        (["r0", "r1", "r2", "r3"], [5, 64, 17, 1]),
-        (["r1", "r3"], [2, 40]),
-        (["r0", "r2", "r3"], [1, 2, 64]),
-        (["r3"], [7]),
-    ]
-    for step, (live, new) in enumerate(schedule):
+    from mstar_amd import _lib
+
+    log(f"BS={BS}: short-query threshold {_lib.lib().mi_prefill_short_rows(BS, HQ, HKV, D)} rows")
+    for step, (live, new) in enumerate(_schedule(BS)):
         ids = live + dummies[len(live):]
         sls = new + [0] * (BS - len(live))
         cm.request_ids = ids
