@@ -149,6 +149,11 @@ MI_DEVICE v4i16 ds_read_tr16(const uint8_t* lds_addr) {
 
 // Wave-uniform value in an SGPR.
 MI_DEVICE int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+MI_DEVICE int64_t uniform64(int64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
 
 MI_DEVICE float xor_shuffle(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 

@@ -20,7 +20,7 @@ constexpr int pf_waves(int) { return 8; }
 constexpr int pf_rg(int head_dim) { return head_dim > 128 ? 1 : 2; }  // 16-row groups per wavefront
 constexpr int pf_rows(int head_dim) { return 16 * pf_rg(head_dim) * pf_waves(head_dim); }  // (token, q-head) rows per workgroup
 constexpr int kPfKeys = 32;                // keys per K/V tile
-constexpr int kPfPageCap = 2048;           // page ids staged in LDS at a time
+constexpr int kPfTileCap = 1024;           // tiles whose row-group addresses are staged in LDS at a time
 constexpr int kCtrStride = 32;  // one 128-byte line per XCD counter
 
 // ------------------------------------------------------------ attention
@@ -74,7 +74,8 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   constexpr int LCH = FP8 ? 32 : 16;  // LDS bytes per loaded chunk
   constexpr float kNegInf = -__builtin_inff();
   __shared__ __attribute__((aligned(16))) uint8_t lds[3 * STAGE];
-  __shared__ int32_t lds_pages[kPfPageCap];
+  // byte offset (from the head's base) of the first row of each 16-row group of the staged tiles
+  __shared__ int64_t lds_toff[2 * kPfTileCap];
 
   __shared__ int s_unit;
   const int nkv = p.num_kv_heads;
@@ -153,6 +154,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // 16, tiles start at multiples of 32): page and slot base are scalars.
   const uint8_t* kvb = (const uint8_t*)p.kv + (int64_t)h * p.head_stride * ESZ;
   const int64_t tok_bytes = p.token_stride * ESZ;
+
   uint32_t l_off[NL];   // per-thread byte offset within (page, first slot of its group)
   int l_grp[NL];        // first key row of the 16-row group (wave-uniform)
   int l_row[NL];        // key row within the tile
@@ -168,7 +170,8 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     l_off[i] = (uint32_t)((int64_t)half * p.kv_stride * ESZ + (int64_t)(row - (row & ~15)) * tok_bytes + 16 * ch);
   }
   const int key_cap = np * ps - 16;  // last 16-row group inside the request's pages
-  int c0 = 0;  // first page of the page ids staged in LDS
+  const int64_t page_bytes = p.page_stride * ESZ;
+  int c0 = 0;  // first tile of the tile addresses staged in LDS
   // NB register buffers: tile X is loaded into buffer (X - t0) % NB, NB steps
   // before the step that stores it to LDS.  Two: with three (loads one step
   // further ahead) the c4 batch ran 1.5-2.5% slower at head_dim 128 (225 vs
@@ -178,29 +181,25 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   constexpr int NB = 2;
   constexpr int UNR = 6;
   uint4 rr[NB][NL];
-  // A tile's loads in two parts: the page ids (LDS reads) and the global
-  // loads, so a step can read its page ids early and issue the loads later.
-  auto tile_pages = [&](int t, int (&pg)[NL]) {
+  // A tile's loads in two parts: the row-group addresses (LDS reads of the
+  // table staged per unit) and the global loads, so a step can read the
+  // addresses early and issue the loads later with no address arithmetic
+  // beyond one add.
+  auto tile_pages = [&](int t, int64_t (&pg)[NL]) {
 #pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      // groups past the request's last page re-read its last group (masked, V zeroed)
-      const int gkey = uniform(min(t * KEYS + l_grp[i], key_cap));
-      pg[i] = lds_pages[gkey / ps - c0];
-    }
+    for (int i = 0; i < NL; ++i) pg[i] = lds_toff[2 * (t - c0) + (l_grp[i] >> 4)];
   };
-  auto load_tile_at = [&](int t, const int (&pg)[NL], uint4 (&r)[NL]) {
+  auto load_tile_at = [&](int t, const int64_t (&pg)[NL], uint4 (&r)[NL]) {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       if (2 * HALF % THREADS == 0 || tid + i * THREADS < 2 * HALF) {
-        const int gkey = uniform(min(t * KEYS + l_grp[i], key_cap));
-        const int page = uniform(pg[i]);
-        const uint8_t* base = kvb + (int64_t)page * p.page_stride * ESZ + (int64_t)(gkey % ps) * tok_bytes;
+        const uint8_t* base = kvb + uniform64(pg[i]);
         r[i] = *(const uint4*)(base + l_off[i]);
       }
     }
   };
   auto load_tile = [&](int t, uint4 (&r)[NL]) {
-    int pg[NL];
+    int64_t pg[NL];
     tile_pages(t, pg);
     load_tile_at(t, pg, r);
   };
@@ -211,9 +210,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       if (2 * HALF % THREADS == 0 || c < 2 * HALF) {
         const int half = c / HALF, rem = c - half * HALF;
         const int row = rem / CPR, ch = rem - row * CPR;
-        uint4 v = r[i];
-        // V rows past the KV end may hold anything (unwritten slots of the last page)
-        if (l_v[i] && t * KEYS + l_row[i] >= kv_len) v = make_uint4(0, 0, 0, 0);
+        const uint4 v = r[i];
         uint8_t* dst = lds + stage * STAGE + (half ? KEYS * RSK + row * RSV : row * RSK) + LCH * ch;
         if constexpr (FP8) {  // 16 fp8 -> 16 MFMA-type elements (32 bytes)
           const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -227,6 +224,15 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
           *(uint4*)(dst + 16) = make_uint4(o[4], o[5], o[6], o[7]);
         } else {
           *(uint4*)dst = v;
+        }
+        // V rows past the KV end may hold anything (unwritten slots of the last
+        // page): only a tile that reaches past kv_len has such rows (a
+        // wave-uniform branch), where they are overwritten with zeros
+        if (t * KEYS + KEYS > kv_len) {
+          if (l_v[i] && t * KEYS + l_row[i] >= kv_len) {
+            *(uint4*)dst = make_uint4(0, 0, 0, 0);
+            if constexpr (FP8) *(uint4*)(dst + 16) = make_uint4(0, 0, 0, 0);
+          }
         }
       }
     }
@@ -392,16 +398,24 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // softmax at the start of step T, group B finishes tile T's at its end.
   const bool grp_a = ((wave ^ (wave >> 2)) & 1) == 0;
 
-  // ---- page chunks (one for contexts up to kPfPageCap pages).  Loads past
-  // the last tile repeat the last tile, so the steady loop has no
-  // conditional loads and the compiler's vmcnt waits stay exact.
-  for (c0 = 0; c0 * ps < kv_end; c0 += kPfPageCap) {
-    const int npg = min(np - c0, kPfPageCap);
+  // ---- tile chunks (one for contexts up to kPfTileCap tiles).  Per chunk,
+  // the byte offset of every tile's two 16-row key groups (page offset plus
+  // slot offset; a group past the request's last page re-reads its last
+  // group, masked and with V zeroed) is staged in LDS, so the step loop does
+  // no page or slot arithmetic.  Loads past the last tile repeat the last
+  // tile, so the steady loop has no conditional loads and the compiler's
+  // vmcnt waits stay exact.
+  for (c0 = 0; c0 * KEYS < kv_end; c0 += kPfTileCap) {
+    const int t0 = c0;
+    const int t1 = min(n_kt, c0 + kPfTileCap);
     __syncthreads();
-    for (int i = tid; i < npg; i += THREADS) lds_pages[i] = p.kv_indices[page_base + c0 + i];
+    for (int e = tid; e < 2 * (t1 - t0); e += THREADS) {
+      const int key = min((t0 + (e >> 1)) * KEYS + 16 * (e & 1), key_cap);
+      const int pidx = (int)((unsigned)key / (unsigned)ps);
+      const int slot = key - pidx * ps;
+      lds_toff[e] = (int64_t)p.kv_indices[page_base + pidx] * page_bytes + (int64_t)slot * tok_bytes;
+    }
     __syncthreads();
-    const int t0 = c0 * ps / KEYS;
-    const int t1 = min(n_kt, (c0 + kPfPageCap) * ps / KEYS);
     const int tl = t1 - 1;
     // Three-stage LDS ring: in step T both groups read V of tile T-1 (P.V)
     // and K of tile T (scores), and tile T+1 is stored into the stage tile
@@ -435,7 +449,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         // Tile T+1 goes into the stage tile T-2 used, which no wave reads in
         // this step; each group stores it (and issues the loads of tile T+1+NB)
         // in its vector half, under the other group's MFMA work.
-        int pg4[NL];
+        int64_t pg4[NL];
         tile_pages(min(T + 1 + NB, tl), pg4);
         // Each group's vector half runs at raised wave priority, so its softmax
         // issues ahead of the partner's MFMA stream on the shared SIMD
