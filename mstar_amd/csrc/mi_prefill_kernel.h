@@ -203,7 +203,9 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     tile_pages(t, pg);
     load_tile_at(t, pg, r);
   };
-  auto store_tile = [&](int t, const uint4 (&r)[NL], int stage) {
+  // TAIL: the tile may reach past kv_len (only the request's last tile can),
+  // so its V rows past the end are overwritten with zeros
+  auto store_tile_impl = [&](int t, const uint4 (&r)[NL], int stage, auto tail) {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int c = tid + i * THREADS;
@@ -225,10 +227,8 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         } else {
           *(uint4*)dst = v;
         }
-        // V rows past the KV end may hold anything (unwritten slots of the last
-        // page): only a tile that reaches past kv_len has such rows (a
-        // wave-uniform branch), where they are overwritten with zeros
-        if (t * KEYS + KEYS > kv_len) {
+        // V rows past the KV end may hold anything (unwritten slots of the last page)
+        if constexpr (decltype(tail)::value) {
           if (l_v[i] && t * KEYS + l_row[i] >= kv_len) {
             *(uint4*)dst = make_uint4(0, 0, 0, 0);
             if constexpr (FP8) *(uint4*)(dst + 16) = make_uint4(0, 0, 0, 0);
@@ -236,6 +236,14 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         }
       }
     }
+  };
+  // Tiles before the request's last one hold no row past kv_len (kv_end <=
+  // kv_len): their stores skip the tail test, chosen by a wave-uniform branch.
+  auto store_tile = [&](int t, const uint4 (&r)[NL], int stage) {
+    if (t * KEYS + KEYS > kv_len)
+      store_tile_impl(t, r, stage, std::true_type{});
+    else
+      store_tile_impl(t, r, stage, std::false_type{});
   };
 
   f32x4 acc[RG][VW];
@@ -250,11 +258,13 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   constexpr float kLazy = 8.f;
   const float lazy_raw = kLazy / sl2;
   float m_run[RG], l_run[RG], thr[RG];  // thr = m_run + lazy_raw
+  float moff[RG];  // -m_run * sl2 (0 while m_run is -inf): the exponent offset, changed only with m_run
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
     m_run[rg] = kNegInf;
     l_run[rg] = 0.f;
     thr[rg] = kNegInf;
+    moff[rg] = 0.f;
   }
 
   // first tile that reaches past some row's limit: (t+1)*KEYS > mask_from
@@ -334,6 +344,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         if (grow) {
           m_run[rg] = mt;
           thr[rg] = mt + lazy_raw;
+          moff[rg] = mt == kNegInf ? 0.f : -mt * sl2;
         }
         l_run[rg] *= alpha;
 #pragma unroll
@@ -344,12 +355,12 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   auto sm_exp = [&](const f32x4 (&s)[RG][2], uint4 (&pb)[RG]) {
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
-      const float moff = m_run[rg] == kNegInf ? 0.f : -m_run[rg] * sl2;
+
       float pr[2][4];
 #pragma unroll
       for (int js = 0; js < 2; ++js)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pr[js][r] = fast_exp2(fmaf(s[rg][js][r], sl2, moff));
+        for (int r = 0; r < 4; ++r) pr[js][r] = fast_exp2(fmaf(s[rg][js][r], sl2, moff[rg]));
       pb[rg] = make_uint4(MT::pack2(pr[0][0], pr[0][1]), MT::pack2(pr[0][2], pr[0][3]),
                           MT::pack2(pr[1][0], pr[1][1]), MT::pack2(pr[1][2], pr[1][3]));
       // row sums of the rounded probabilities the PV product uses
