@@ -241,8 +241,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   const uint32_t vrow = (uint32_t)(p.token_stride * ESZ);
   const int64_t kvhalf = p.kv_stride * ESZ;
 
+  // page ids, slots and strides are non-negative: unsigned scalar arithmetic
+  // (a signed division and 64-bit multiply per tile cost ~30 scalar ops)
+  const uint64_t page_bytes = (uint64_t)p.page_stride * ESZ;
   auto tile_base = [&](int page, int r0) -> const uint8_t* {
-    return kv + (int64_t)page * p.page_stride * ESZ + (int64_t)r0 * p.token_stride * ESZ + head_off;
+    return kv + (uint64_t)(uint32_t)page * page_bytes + (uint32_t)r0 * vrow + head_off;
   };
   auto load_tile = [&](TileRegs<FP8, D>& t, const uint8_t* base) {
     const uint8_t* kb = base + voff0;
@@ -374,12 +377,13 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   // MFMA work (three register buffers).
   for (int w0 = 0; w0 < ntiles;) {
     const int wtok = tok_begin + 16 * w0;  // first token of the window
-    const int first = wtok / ps;           // its page (request-relative)
+    const int first = (int)((unsigned)wtok / (unsigned)ps);  // its page (request-relative)
     const int wt = min(ntiles - w0, ((first + 64) * ps - wtok) >> 4);
     const int pwin = first + lane < pg1 ? p.kv_indices[page_base + first + lane] : 0;
     auto tile_ptr = [&](int t) -> const uint8_t* {  // t: tile within the window
-      const int tok = wtok + 16 * t;
-      return tile_base(__builtin_amdgcn_readlane(pwin, tok / ps - first), tok % ps);
+      const unsigned tok = (unsigned)(wtok + 16 * t);
+      const unsigned pg = tok / (unsigned)ps;
+      return tile_base(__builtin_amdgcn_readlane(pwin, (int)pg - first), (int)(tok - pg * (unsigned)ps));
     };
     TileRegs<FP8, D> A, B, C;
     load_tile(A, tile_ptr(0));
