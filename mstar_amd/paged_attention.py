@@ -89,9 +89,13 @@ class _Staging:
         buf = self.bufs[i]
         if buf is None or buf.numel() < total:
             buf = self.bufs[i] = torch.empty(max(total, 1 << 16), dtype=torch.int32, pin_memory=True)
+        # numpy copies on the calling thread: torch's CPU copy_ of a part above
+        # its grain size wakes the intra-op thread pool, which cost 0.1-0.7 ms
+        # per plan on a box whose pool had been resized
+        host = buf.numpy()
         off = 0
         for f, n in zip(flat, sizes):
-            buf[off:off + n].copy_(f)
+            host[off:off + n] = f.numpy()
             off += n
         cur = torch.cuda.current_stream(device)
         if torch.cuda.is_current_stream_capturing():  # a captured plan keeps the copy on its own stream
