@@ -262,3 +262,49 @@ def test_decode_paired_plan_with_padded_heads(gpu):
     err = max_abs(out, ref)
     log(f"decode paired plan, padded heads: max_abs={err:.3e}")
     assert err < TOL_BF16
+
+
+def _index_variants(arrays):
+    """The same index arrays as the plan may receive them: int32 contiguous
+    (the reference's), int64, int32 strided views, and device tensors."""
+    def strided(a):
+        wide = np.repeat(np.asarray(a, dtype=np.int32), 2)  # every element twice
+        return torch.from_numpy(wide)[::2]
+    return {
+        "int32": [torch.as_tensor(np.asarray(a, dtype=np.int32)) for a in arrays],
+        "int64": [torch.as_tensor(np.asarray(a, dtype=np.int64)) for a in arrays],
+        "strided": [strided(a) for a in arrays],
+        "device": None,  # filled per device by the caller
+    }
+
+
+def test_decode_plan_index_inputs(gpu):
+    """plan() over int64, strided and device index tensors gives bit-identical
+    outputs and write locations to int32 contiguous CPU tensors (the staging
+    copy into pinned memory and the device conversion paths)."""
+    hq, hkv, d, ps = 32, 4, 128, 16
+    lens = [1, 17, 300, 1000, 2500, 64]
+    _, kv_indptr, kv_indices, last = custom_batch(lens, ps, 400, seed=3)
+    g = torch.Generator().manual_seed(11)
+    cache0 = random_cache(400, ps, hkv, d, 3).to(gpu)
+    q = torch.randn(len(lens), hq, d, generator=g).to(torch.bfloat16).to(gpu)
+    k_new = torch.randn(len(lens), hkv, d, generator=g).to(torch.bfloat16).to(gpu)
+    v_new = torch.randn(len(lens), hkv, d, generator=g).to(torch.bfloat16).to(gpu)
+    variants = _index_variants([kv_indptr, kv_indices, last])
+    variants["device"] = [t.to(gpu) for t in variants["int32"]]
+    results = {}
+    for name, idx in variants.items():
+        assert name != "strided" or not idx[1].is_contiguous()
+        cache = cache0.clone()
+        w = FlashInferDecodeWrapper(workspace(gpu), hq, hkv, d, ps, device=gpu)
+        w.plan(*idx, dtype=torch.bfloat16)
+        w.set_kv_cache(cache, k_new, v_new)
+        out = w.run(q, cache)
+        torch.cuda.synchronize()
+        results[name] = (out.cpu(), w.kv_cache_locations.cpu(), cache.cpu())
+        log(f"decode plan index inputs: {name}")
+    base = results["int32"]
+    for name, (out, loc, cache) in results.items():
+        assert torch.equal(out.view(torch.int16), base[0].view(torch.int16)), name
+        assert torch.equal(loc, base[1]), name
+        assert torch.equal(cache.view(torch.int16), base[2].view(torch.int16)), name

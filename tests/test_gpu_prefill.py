@@ -346,3 +346,42 @@ def test_prefill_long_context_page_chunks(gpu, hq, hkv, d, causal):
     err = (out.float() - ref).abs().max().item()
     log(f"  max_abs={err:.3e}")
     assert err < TOL
+
+
+def test_prefill_plan_index_inputs(gpu):
+    """plan() over int64, strided and device index tensors gives bit-identical
+    outputs and appended pages to int32 contiguous CPU tensors."""
+    hq, hkv, d, ps = 28, 4, 128, 16
+    kv_lens, new_lens = [40, 700, 1300, 33], [40, 1, 600, 2]
+    qo, kv_indptr, kv_indices, last = custom_batch(kv_lens, ps, 200, seed=5, new_lens=new_lens)
+    ntok = int(qo[-1])
+    g = torch.Generator().manual_seed(13)
+    cache0 = random_cache(200, ps, hkv, d, 5).to(gpu)
+    q = torch.randn(ntok, hq, d, generator=g).to(torch.bfloat16).to(gpu)
+    k = torch.randn(ntok, hkv, d, generator=g).to(torch.bfloat16).to(gpu)
+    v = torch.randn(ntok, hkv, d, generator=g).to(torch.bfloat16).to(gpu)
+
+    def strided(a):
+        return torch.from_numpy(np.repeat(np.asarray(a, dtype=np.int32), 2))[::2]
+
+    arrays = [qo, kv_indptr, kv_indices, last]
+    variants = {
+        "int32": [torch.as_tensor(np.asarray(a, dtype=np.int32)) for a in arrays],
+        "int64": [torch.as_tensor(np.asarray(a, dtype=np.int64)) for a in arrays],
+        "strided": [strided(a) for a in arrays],
+    }
+    variants["device"] = [t.to(gpu) for t in variants["int32"]]
+    results = {}
+    for name, idx in variants.items():
+        cache = cache0.clone()
+        w = FlashInferPrefillWrapper(workspace(gpu), hq, hkv, d, ps, device=gpu)
+        w.plan(*idx, causal=True, dtype=torch.bfloat16)
+        w.set_kv_cache(cache, k, v)
+        out = w.run(q, cache)
+        torch.cuda.synchronize()
+        results[name] = (out.cpu(), cache.cpu())
+        log(f"prefill plan index inputs: {name}")
+    base = results["int32"]
+    for name, (out, cache) in results.items():
+        assert torch.equal(out.view(torch.int16), base[0].view(torch.int16)), name
+        assert torch.equal(cache.view(torch.int16), base[1].view(torch.int16)), name
