@@ -214,18 +214,17 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
   // Keys >= mask_from need a per-row check (uniform bound).
   const int mask_from = p.causal ? (kv_len - qo_len + 1) : kv_len;
 
-  // ---- Q as the B operand of S^T = K Q^T: lane holds Q[row col][8*grp + 32*s ...]
-  uint4 qf[KS];
+  // ---- Q as the B operand of S^T = K Q^T: lane holds Q[row col][8*grp + 32*s ...].
+  // PAIR: only the row's own 128 elements; both heads' score products use
+  // them, and each column keeps the product with its own head's keys.
+  constexpr int QS = PAIR ? KS / 2 : KS;
+  uint4 qf[QS];
   {
     const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(qo_start + qtok) * p.q_stride_tok +
                            (int64_t)(hq * G + g) * p.q_stride_head;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      // PAIR: the row's 128 elements sit in its half of the 256, zeros in the other
-      const int sr = PAIR ? s - (KS / 2) * half : s;
-      const bool in = PAIR ? (sr >= 0 && sr < KS / 2) : true;
-      qf[s] = row_valid && in ? *(const uint4*)(qrow + 32 * sr + 8 * grp) : make_uint4(0, 0, 0, 0);
-    }
+    for (int s = 0; s < QS; ++s)
+      qf[s] = row_valid ? *(const uint4*)(qrow + 32 * s + 8 * grp) : make_uint4(0, 0, 0, 0);
   }
   float kscale = 1.0f, vscale = 1.0f;
   if constexpr (FP8) {
@@ -290,17 +289,18 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     // ---- S^T = K . Q^T  (A fragment: row col, elements 8*grp + 32*st .. +8)
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     if constexpr (PAIR) {
-      // One accumulator per head of the pair (k-steps [0, KS/2) are head 2h's
-      // elements, [KS/2, KS) head 2h+1's); each column keeps its own head's,
-      // so a non-finite key of one head never reaches the other head's scores
-      // through 0 * Inf.
+      // One accumulator per head of the pair: s takes the keys' k-steps
+      // [0, KS/2) (head 2h's elements), s1 the k-steps [KS/2, KS) (head
+      // 2h+1's), both against the row's own 128 query elements.  A column
+      // keeps the product with its own head's keys (a select, so the other
+      // product's values, non-finite ones included, never reach it).
       f32x4 s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < KS / 2; ++st) {
         const uint4 a0 = *(const uint4*)(kst + col * KRS + (8 * grp + 32 * st) * 2);
         const uint4 a1 = *(const uint4*)(kst + col * KRS + (8 * grp + 32 * (st + KS / 2)) * 2);
         s = MT::mma_16x16x32(a0, qf[st], s);
-        s1 = MT::mma_16x16x32(a1, qf[st + KS / 2], s1);
+        s1 = MT::mma_16x16x32(a1, qf[st], s1);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[r] = half ? s1[r] : s[r];
