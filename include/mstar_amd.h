@@ -45,7 +45,7 @@ extern "C" {
 #define MI_ERR_WORKSPACE (-3)   /* workspace too small or not planned for this call */
 #define MI_ERR_LAUNCH (-4)      /* HIP launch error */
 
-#define MI_ABI_VERSION 3
+#define MI_ABI_VERSION 4
 
 /* One layer of the paged KV cache. Strides are in elements. */
 typedef struct mi_paged_kv {
@@ -115,13 +115,20 @@ int mi_pack_plan(const int32_t* req_slot, const int32_t* seq_len, const int32_t*
 
 /* mi_pack_plan (workspace != NULL) or mi_pack (workspace == NULL) with the step's
  * metadata in HOST memory, handed to the kernel as its launch argument instead of being
- * copied to the device first: meta holds meta_len <= MI_PACK_HOST_META int32 values,
+ * copied to the device first: meta holds meta_len int32 values,
  * [req_slot | seq_len | new_len | num_pages | table_pages] (batch values each, in that
  * order) followed by the new pages (as many as the num_pages - table_pages differences
  * add up to, else MI_ERR_INVALID); the buffer may be reused once the call returns.
+ * meta_len <= MI_PACK_HOST_META is always accepted.  Up to MI_PACK_HOST_META_MAX values
+ * are accepted when the step fits the argument in a compact form (every req_slot,
+ * new_len, num_pages and table_pages below 65536, two of them per int32, and
+ * 3 * batch + new pages <= MI_PACK_HOST_ARGS); otherwise the call returns
+ * MI_ERR_UNSUPPORTED without launching anything and the caller uses mi_pack_plan.
  * Same outputs as the device-pointer entry points.  Extension for small steps (no
  * counterpart in the reference): it saves the host-to-device copy of the metadata. */
 #define MI_PACK_HOST_META 768
+#define MI_PACK_HOST_META_MAX 4096
+#define MI_PACK_HOST_ARGS 896
 int mi_pack_plan_host(const int32_t* meta, int32_t meta_len, int32_t batch, int32_t* block_table,
                       int64_t block_table_stride, int32_t page_size, int32_t* qo_indptr,
                       int32_t* kv_indptr, int32_t* kv_indices, int32_t* last_page_len,

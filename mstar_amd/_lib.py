@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded before the HIP library, see above)
 
 LIB_PATH = Path(__file__).resolve().parent / "libmstar_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # dtype codes (mstar_amd.h)
 MI_BF16 = 0
@@ -256,7 +256,9 @@ def _event_create(device: torch.device) -> int:
     return ev.value
 
 
-PACK_HOST_META = 768  # MI_PACK_HOST_META: int32 values of step metadata passed as a kernel argument
+PACK_HOST_META = 768  # MI_PACK_HOST_META: int32 values of step metadata always passed as a kernel argument
+PACK_HOST_META_MAX = 4096  # MI_PACK_HOST_META_MAX: up to this many when the step fits the argument's compact form
+MI_ERR_UNSUPPORTED = -2
 
 
 class PinnedUploader:

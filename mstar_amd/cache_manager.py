@@ -237,15 +237,18 @@ class BatchedCacheManager:
                      ws.numel() * ws.element_size() if ws is not None else 0)
         loc_ptr = loc.data_ptr() if loc is not None else None
         ps = self.kv_cache_config.page_size
-        if meta.size <= _lib.PACK_HOST_META:
-            # small step: the metadata travels as the kernel's argument, no copy to the device
+        if meta.size <= _lib.PACK_HOST_META_MAX:
+            # a step whose metadata fits the kernel's argument (as given up to
+            # PACK_HOST_META values, compact beyond): no copy to the device
             meta = np.ascontiguousarray(meta, dtype=np.int32)
-            bt.launch(lambda table: _lib.check(
-                _lib.lib().mi_pack_plan_host(
-                    meta.ctypes.data, meta.size, b, table, bt.stride, ps, qo.data_ptr(), kv_indptr.data_ptr(),
-                    kv_indices.data_ptr(), last.data_ptr(), loc_ptr, grid, *plan_args, stream),
-                "mi_pack_plan_host"))
-            return
+            rc = bt.launch(lambda table: _lib.lib().mi_pack_plan_host(
+                meta.ctypes.data, meta.size, b, table, bt.stride, ps, qo.data_ptr(), kv_indptr.data_ptr(),
+                kv_indices.data_ptr(), last.data_ptr(), loc_ptr, grid, *plan_args, stream))
+            if rc == _lib.MI_OK:
+                return
+            if rc != _lib.MI_ERR_UNSUPPORTED or meta.size <= _lib.PACK_HOST_META:
+                _lib.check(rc, "mi_pack_plan_host")
+            # too large for the argument: the metadata goes to the device below
         dmeta = self._pack.upload(meta)
         base = dmeta.data_ptr()
 

@@ -129,26 +129,51 @@ __global__ __launch_bounds__(kPackThreads) void pack_plan_kernel(PackParams p, P
 }
 
 // The step's metadata as a kernel argument (mi_pack_plan_host): up to
-// MI_PACK_HOST_META int32 values, [slot | seq_len | new_len | num_pages |
-// pages on the device] (batch each) followed by the new pages.
+// MI_PACK_HOST_ARGS int32 values, either as given, [slot | seq_len | new_len |
+// num_pages | pages on the device] (batch each) followed by the new pages, or
+// compact, [seq_len | slot + num_pages * 2^16 | new_len + pages on the device
+// * 2^16] (batch each) followed by the new pages.
+static_assert(MI_PACK_HOST_ARGS >= MI_PACK_HOST_META, "the argument holds any metadata of MI_PACK_HOST_META values");
+constexpr int kHostCompactMax = MI_PACK_HOST_ARGS / 3;  // requests of a compact step
 struct HostMeta {
-  int32_t v[MI_PACK_HOST_META];
+  int32_t v[MI_PACK_HOST_ARGS];
 };
 
-// pack_plan_kernel over the argument copy; with_plan == 0: pack only (no plan workgroup).
+// pack_plan_kernel over the argument copy; with_plan == 0: pack only (no plan
+// workgroup).  Every workgroup copies the per-request fields but seq_len into
+// LDS (unpacking the compact form), so each of the kernel's array pointers
+// has one address space whichever form arrived (a pointer that could be
+// either the argument or LDS made the compiler copy the whole argument to
+// scratch memory in every lane).
 __global__ __launch_bounds__(kPackThreads) void pack_plan_host_kernel(PackParams p, PlanParams pl, HostMeta m,
-                                                                      int32_t with_plan) {
+                                                                      int32_t with_plan, int32_t compact) {
+  __shared__ int32_t s_meta[4][kHostCompactMax];
   const int32_t* base = m.v;
   const int b = p.batch;
-  p.req_slot = base;
-  p.seq_len = base + b;
-  p.new_len = base + 2 * b;
-  p.num_pages = base + 3 * b;
-  p.table_pages = base + 4 * b;
-  p.new_pages = base + 5 * b;
+  for (int r = (int)threadIdx.x; r < b; r += kPackThreads) {
+    if (compact) {
+      const uint32_t a = (uint32_t)base[b + r], c = (uint32_t)base[2 * b + r];
+      s_meta[0][r] = (int32_t)(a & 0xffffu);  // slot
+      s_meta[1][r] = (int32_t)(c & 0xffffu);  // new tokens
+      s_meta[2][r] = (int32_t)(a >> 16);      // pages
+      s_meta[3][r] = (int32_t)(c >> 16);      // pages on the device
+    } else {
+      s_meta[0][r] = base[r];
+      s_meta[1][r] = base[2 * b + r];
+      s_meta[2][r] = base[3 * b + r];
+      s_meta[3][r] = base[4 * b + r];
+    }
+  }
+  __syncthreads();
+  p.req_slot = s_meta[0];
+  p.new_len = s_meta[1];
+  p.num_pages = s_meta[2];
+  p.table_pages = s_meta[3];
+  p.seq_len = compact ? base : base + b;
+  p.new_pages = base + (compact ? 3 : 5) * b;
   if (with_plan) {
     if (blockIdx.x == 0) {
-      pl.num_pages = base + 3 * b;
+      pl.num_pages = p.num_pages;
       decode_plan_body(pl);
       return;
     }
@@ -242,17 +267,33 @@ extern "C" int mi_pack_plan_host(const int32_t* meta, int32_t meta_len, int32_t 
                                  int32_t num_kv_heads, int32_t head_dim, void* workspace, int64_t workspace_bytes,
                                  void* stream) {
   using namespace mi;
-  if (!meta || batch < 0 || meta_len > MI_PACK_HOST_META || (int64_t)meta_len < 5LL * batch) return MI_ERR_INVALID;
+  if (!meta || batch < 0 || meta_len > MI_PACK_HOST_META_MAX || (int64_t)meta_len < 5LL * batch)
+    return MI_ERR_INVALID;
   // the new pages the kernel will read are exactly the ones meta carries
   int64_t new_pages = 0;
+  bool fits16 = true;  // slot, new tokens, pages and pages on the device below 2^16
   for (int32_t r = 0; r < batch; ++r) {
-    const int32_t np = meta[3 * batch + r], old = meta[4 * batch + r];
+    const int32_t slot = meta[r], sl = meta[2 * batch + r], np = meta[3 * batch + r], old = meta[4 * batch + r];
     if (np < 0 || old < 0) return MI_ERR_INVALID;
     new_pages += np - (old < np ? old : np);
+    fits16 = fits16 && (uint32_t)slot < 65536u && (uint32_t)sl < 65536u && np < 65536 && old < 65536;
   }
   if (new_pages != (int64_t)meta_len - 5LL * batch) return MI_ERR_INVALID;
   HostMeta m;
-  memcpy(m.v, meta, sizeof(int32_t) * (size_t)meta_len);
+  int32_t compact = 0;
+  if (meta_len <= MI_PACK_HOST_ARGS) {
+    memcpy(m.v, meta, sizeof(int32_t) * (size_t)meta_len);
+  } else if (fits16 && batch <= kHostCompactMax && 3LL * batch + new_pages <= MI_PACK_HOST_ARGS) {
+    compact = 1;
+    for (int32_t r = 0; r < batch; ++r) {
+      m.v[r] = meta[batch + r];
+      m.v[batch + r] = (int32_t)((uint32_t)meta[r] | ((uint32_t)meta[3 * batch + r] << 16));
+      m.v[2 * batch + r] = (int32_t)((uint32_t)meta[2 * batch + r] | ((uint32_t)meta[4 * batch + r] << 16));
+    }
+    memcpy(m.v + 3 * batch, meta + 5 * batch, sizeof(int32_t) * (size_t)new_pages);
+  } else {
+    return MI_ERR_UNSUPPORTED;  // the caller copies the metadata to the device (mi_pack_plan)
+  }
   // pointers for the argument checks only: the kernel points them at its copy of meta
   const int32_t* chk = batch > 0 ? meta : nullptr;
   PackParams pp{};
@@ -267,7 +308,7 @@ extern "C" int mi_pack_plan_host(const int32_t* meta, int32_t meta_len, int32_t 
     if (st != MI_OK) return st;
   }
   hipLaunchKernelGGL(pack_plan_host_kernel, dim3(grid_blocks + with_plan), dim3(kPackThreads), 0,
-                     (hipStream_t)stream, pp, pl, m, with_plan);
+                     (hipStream_t)stream, pp, pl, m, with_plan, compact);
   MI_CHECK_LAUNCH();
   return MI_OK;
 }

@@ -263,7 +263,7 @@ def test_pack_plan_host_arguments_are_checked(L):
         return L.mi_pack_plan_host(meta_ptr, meta_len, batch, p, 8, 16, p, p, p, p, None, grid, 32, 4, 128, ws,
                                    1 << 30, None)
 
-    assert call(meta_len=769) == MI_ERR_INVALID        # more than MI_PACK_HOST_META values
+    assert call(meta_len=4097) == MI_ERR_INVALID       # more than MI_PACK_HOST_META_MAX values
     meta[12] = 3                                       # request 0 holds 3 pages, none in the table:
     assert call(meta_len=20) == MI_ERR_INVALID         # 3 new pages expected, none given
     meta[12] = 0
@@ -271,3 +271,13 @@ def test_pack_plan_host_arguments_are_checked(L):
     assert call(meta_ptr=None) == MI_ERR_INVALID       # no metadata
     assert call(grid=0) == MI_ERR_INVALID              # pack: no workgroups
     assert call(grid=0, ws=None) == MI_ERR_INVALID     # pack only: same checks
+
+    # beyond MI_PACK_HOST_ARGS values: only a step that fits the compact form is launched
+    big = (ctypes.c_int32 * 4096)()
+    bm = ctypes.cast(big, ctypes.c_void_p)
+    assert call(meta_len=5 * 300, batch=300, meta_ptr=bm) == MI_ERR_UNSUPPORTED  # 3 * 300 > 896 values
+    big[0] = 70000                                                             # a slot above 2^16
+    assert call(meta_len=5 * 200, batch=200, meta_ptr=bm) == MI_ERR_UNSUPPORTED
+    big[0] = 0
+    big[3 * 200] = 2                                                           # 2 pages, 2 new ones given
+    assert call(meta_len=5 * 200 + 1, batch=200, meta_ptr=bm) == MI_ERR_INVALID  # counts disagree

@@ -153,14 +153,17 @@ def test_decode_plan_partition(gpu, lens, pool, hq, hkv):
 
 
 @pytest.mark.parametrize("with_plan", [True, False])
-def test_pack_plan_host_matches_device_metadata(gpu, with_plan):
+@pytest.mark.parametrize("nreq", [64, 200])
+def test_pack_plan_host_matches_device_metadata(gpu, with_plan, nreq):
     """mi_pack_plan_host (metadata as the kernel argument) == mi_pack_plan / mi_pack with
-    the same metadata in device memory: packed arrays, table rows and plan."""
+    the same metadata in device memory: packed arrays, table rows and plan.  64 requests
+    pass the metadata as given, 200 requests (more than MI_PACK_HOST_ARGS values) in the
+    argument's compact form."""
     from mstar_amd.cache_manager import _step_tensors
 
     ps, hq, hkv, d = 16, 24, 8, 128
     rng = np.random.default_rng(11)
-    lens = [0, 1, 16, 17] + rng.integers(1, 3000, size=60).tolist()
+    lens = [0, 1, 16, 17] + rng.integers(1, 3000, size=nreq - 4).tolist()
     b = len(lens)
     npages = np.array([(t + ps - 1) // ps for t in lens], dtype=np.int32)
     # a decode step: all but the last page or two of each list are already in the table
@@ -180,7 +183,10 @@ def test_pack_plan_host_matches_device_metadata(gpu, with_plan):
     meta[3] = npages
     meta[4] = old
     flat = np.concatenate([meta.reshape(-1)] + new_pages).astype(np.int32)
-    assert flat.size <= _lib.PACK_HOST_META
+    if nreq == 64:
+        assert flat.size <= _lib.PACK_HOST_META
+    else:  # beyond the argument as given, within its compact form
+        assert flat.size > 896 and 3 * b + (flat.size - 5 * b) <= 896
     dmeta = torch.from_numpy(flat).to(gpu)
     base = dmeta.data_ptr()
     table0 = np.zeros((b, stride), dtype=np.int32)
@@ -208,7 +214,19 @@ def test_pack_plan_host_matches_device_metadata(gpu, with_plan):
         torch.cuda.synchronize()
         outs.append(([t.cpu().tolist() for t in (qo, ip, idx, last, loc)], table.cpu().tolist(),
                      ws[:1 << 16].cpu().tolist() if with_plan else None))
-    assert outs[0] == outs[1]
+    assert outs[0][:2] == outs[1][:2]
+    if with_plan:
+        # The plan: header and item offsets equal; the work list equal as a set
+        # (items of one size bucket are placed by LDS atomics, whose order across
+        # the plan workgroup's wavefronts varies from run to run).
+        ws0, ws1 = (np.array(o[2], dtype=np.uint8).view(np.int32) for o in outs)
+        assert ws0[:5].tolist() == ws1[:5].tolist()
+        ci = 64  # item offsets at byte 256
+        assert ws0[ci:ci + b + 1].tolist() == ws1[ci:ci + b + 1].tolist()
+        wk = -(-(256 + 4 * (b + 1)) // 256) * 64  # work list, 256-byte aligned after the offsets
+        n = int(ws0[2])
+        w0, w1 = (sorted(map(tuple, w[wk:wk + 4 * n].reshape(-1, 4).tolist())) for w in (ws0, ws1))
+        assert w0 == w1
     # and the packed page lists are the requests' lists
     ip_h, idx_h = np.array(outs[1][0][1]), np.array(outs[1][0][2])
     for r in range(b):
