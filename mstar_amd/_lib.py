@@ -28,6 +28,7 @@ MI_I32 = 4
 MI_I64 = 5
 
 MI_OK = 0
+MI_ERR_UNSUPPORTED = -2
 
 TORCH_TO_MI = {
     torch.bfloat16: MI_BF16,
@@ -258,7 +259,6 @@ def _event_create(device: torch.device) -> int:
 
 PACK_HOST_META = 768  # MI_PACK_HOST_META: int32 values of step metadata always passed as a kernel argument
 PACK_HOST_META_MAX = 4096  # MI_PACK_HOST_META_MAX: up to this many when the step fits the argument's compact form
-MI_ERR_UNSUPPORTED = -2
 
 
 class PinnedUploader:
