@@ -768,6 +768,9 @@ def bench_prefill(args, dev) -> dict:
                                  "GBps": short_bytes / (float(short_ms.mean()) * 1e-3) / 1e9},
         },
     }
+    gemm = library_gemm(dev)
+    res["roofline"]["library_gemm"] = gemm
+    res["roofline"]["frac_of_library_gemm"] = achieved / gemm["TFLOPs"]
     if not args.no_extra:
         res["prefill_head_dim_256"] = bench_prefill_d256(dev, args.steps)
         res["prefill_fp8_kv"] = bench_prefill_fp8(w, q, layer, s, dev, args.steps, long_f)
@@ -814,6 +817,22 @@ def bench_prefill_vs_sdpa(dev, steps: int) -> dict:
             "torch_sdpa_us": us_sdpa, "torch_sdpa_frac": flops / us_sdpa / 1e6 / MFMA_BF16_PEAK_TFLOPS,
             "paged_prefill_us": us_ours, "paged_prefill_frac": flops / us_ours / 1e6 / MFMA_BF16_PEAK_TFLOPS,
             "max_abs_diff": diff}
+
+
+def library_gemm(dev, n: int = 16384, steps: int = 5) -> dict:
+    """The box's practical matrix-core ceiling for reference: a square bf16
+    GEMM through torch.matmul (hipBLASLt), n^3, HIP events, right after the
+    prefill timing (same clock and thermal state)."""
+    g = torch.Generator(device=dev).manual_seed(11)
+    a = torch.randn(n, n, device=dev, generator=g).to(torch.bfloat16)
+    b = torch.randn(n, n, device=dev, generator=g).to(torch.bfloat16)
+    for _ in range(2):
+        a @ b
+    us = _run_us(lambda: a @ b, steps)
+    del a, b
+    tf = 2 * n ** 3 / us / 1e6
+    return {"what": f"torch.matmul bf16 {n}x{n}x{n} (hipBLASLt)", "us": us, "TFLOPs": tf,
+            "frac": tf / MFMA_BF16_PEAK_TFLOPS}
 
 
 def _run_us(fn, steps: int) -> float:
@@ -918,6 +937,8 @@ def side_configs(args, dev) -> dict:
                 "algorithmic_flops": rf["algorithmic_flops"], "TFLOPs": rf["achieved"],
                 "mfma_frac": rf["frac"], "short_query_us": sq["us"], "short_query_bytes": sq["algorithmic_bytes"],
                 "short_query_GBps": sq["GBps"], "short_query_hbm_frac": sq["GBps"] / HBM_PEAK_GBS,
+                "library_gemm_TFLOPs": rf["library_gemm"]["TFLOPs"],
+                "mfma_frac_of_library_gemm": rf["frac_of_library_gemm"],
             }
         else:
             r = bench_decode(sub, dev)
