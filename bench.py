@@ -342,6 +342,29 @@ WORKLOADS = {
 }
 
 
+def hbm_read_ceiling(buf: torch.Tensor, steps: int = 10) -> dict:
+    """The box's plain read rate over ``buf`` (the KV pool layer the decode
+    kernel streams): ``mi_hbm_read`` with the decode kernel's 16-byte
+    non-temporal loads, median of ``steps`` launches timed with HIP events."""
+    dev = buf.device
+    nbytes = buf.numel() * buf.element_size() // 16 * 16
+    grid = 8 * torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.empty(4 * grid, dtype=torch.int32, device=dev)
+    stream = _lib.stream_ptr(dev)
+    launch = lambda: _lib.check(_lib.lib().mi_hbm_read(buf.data_ptr(), nbytes, sink.data_ptr(), grid, stream),
+                                "mi_hbm_read")
+    launch()
+    evs = _kernel_events(steps, 2)
+    for e0, e1 in evs:
+        e0.record()
+        launch()
+        e1.record()
+    torch.cuda.synchronize()
+    us = float(np.median([e0.elapsed_time(e1) for e0, e1 in evs])) * 1e3
+    return {"kernel": "hbm_read_kernel", "what": "plain 16-byte non-temporal read of the KV pool layer",
+            "bytes": nbytes, "us_median": us, "GBps": nbytes / (us * 1e-6) / 1e9}
+
+
 def _kernel_events(n: int, k: int):
     return [tuple(torch.cuda.Event(enable_timing=True) for _ in range(k)) for _ in range(n)]
 
@@ -384,6 +407,7 @@ def bench_decode(args, dev) -> dict:
     dec_us, dm_us = decode_graph_us(cm, q, args.steps)
     achieved = graph_bytes / (dec_us * 1e-6) / 1e9
     kv_tokens = int(seq_now.sum())
+    ceiling = hbm_read_ceiling(kv[0])
     lo, hi = s.ctx[1], s.ctx[2]
     traffic, traffic_alg = measured_traffic(s.name)
     res = {
@@ -424,6 +448,8 @@ def bench_decode(args, dev) -> dict:
             "kernel_us_events_in_step_loop": float(dec_ms.mean()) * 1e3,
             "decode_plus_merge_us_events_in_step_loop": float(dm_ms.mean()) * 1e3,
             "algorithmic_bytes_step_loop_mean": int(np.mean(bytes_per)),
+            "hbm_read_ceiling": ceiling,
+            "frac_of_read_ceiling": achieved / ceiling["GBps"],
         },
     }
     pos_now = seq_now
@@ -948,6 +974,7 @@ def side_configs(args, dev) -> dict:
                 "steps": sub.steps, "ms_per_step": r["ms_per_step"], "tokens_per_s": r["value"],
                 "kernel": rf["kernel"], "kernel_us": rf["kernel_us"], "decode_plus_merge_us": rf["decode_plus_merge_us"],
                 "algorithmic_bytes": rf["algorithmic_bytes"], "GBps": rf["achieved"], "hbm_frac": rf["frac"],
+                "read_ceiling_GBps": rf["hbm_read_ceiling"]["GBps"], "frac_of_read_ceiling": rf["frac_of_read_ceiling"],
             }
         _log(f"{name}: " + json.dumps({k: v for k, v in out[name].items() if k != "workload"}))
     return out

@@ -433,6 +433,14 @@ int mi_kv_wire_unpack(const void* wire, int64_t wire_bytes, const mi_kv_pool* po
                       const int32_t* token_start, const int32_t* token_end, const int64_t* row_offset,
                       int32_t num_records, int32_t layer_begin, int32_t layer_end, void* stream);
 
+/* Measurement only (no counterpart in the reference): reads `bytes` (a
+ * multiple of 16, `data` 16-byte aligned) of device memory with the decode
+ * kernels' 16-byte non-temporal loads, `grid` workgroups of 256 threads, and
+ * writes one folded word per wavefront to sink[0 .. 4*grid).  Its rate over a
+ * KV pool is the box's plain HBM read ceiling, which the benchmark reports
+ * beside the decode kernel's achieved bandwidth. */
+int mi_hbm_read(const void* data, int64_t bytes, uint32_t* sink, int32_t grid, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

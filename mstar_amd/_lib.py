@@ -152,6 +152,7 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _I64, ctypes.POINTER(MiKvPool), _P, _P, _P, _P, _I32, _I32, _I32, _P],
     ),
+    "mi_hbm_read": (ctypes.c_int, [_P, _I64, _P, _I32, _P]),
     "mi_rope_apply": (
         ctypes.c_int,
         [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _I32, _I32, _I32, _F32, _F32,

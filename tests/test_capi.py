@@ -198,6 +198,13 @@ def test_transfer_arguments_are_checked(L):
     assert L.mi_kv_copy_tokens(good, good, p, p, None, None, -1, 0, 1, None) == MI_ERR_INVALID
     assert L.mi_kv_copy_tokens(good, good, p, p, p, None, 1, 0, 1, None) == MI_ERR_INVALID
     assert L.mi_kv_wire_pack(good, p, p, None, None, 1, 0, 1, p, 64, None) == MI_ERR_INVALID
+    # the HBM read probe: null buffers, sizes that are not whole 16-byte pieces, misalignment, no grid
+    assert L.mi_hbm_read(None, 16, p, 1, None) == MI_ERR_INVALID
+    assert L.mi_hbm_read(p, 16, None, 1, None) == MI_ERR_INVALID
+    assert L.mi_hbm_read(p, 20, p, 1, None) == MI_ERR_INVALID
+    assert L.mi_hbm_read(4100, 16, p, 1, None) == MI_ERR_INVALID
+    assert L.mi_hbm_read(p, 0, p, 1, None) == MI_ERR_INVALID
+    assert L.mi_hbm_read(p, 16, p, 0, None) == MI_ERR_INVALID
 
 
 def test_noalloc_decode_rejects_oversized_batch_on_the_host(L):
