@@ -918,7 +918,7 @@ def bench_prefill_d256(dev, steps: int) -> dict:
     torch.cuda.synchronize()
     us = float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3
     flops = sum(4 * hq * d * (kl - n + t + 1) for kl, n in zip(kv_lens, new) for t in range(n))
-    return {"kernel": "prefill_kernel<BF16, false, 256>", "us": us, "algorithmic_flops": flops,
+    return {"kernel": "prefill_rs_kernel<BF16, false>", "us": us, "algorithmic_flops": flops,
             "TFLOPs": flops / us / 1e6, "frac": flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS}
 
 

@@ -12,22 +12,27 @@
 //        requests) and mi_prefill_tiles (prefill_kernel).
 //
 // prefill_kernel (persistent, one workgroup per CU): a unit is a tile of
-// 256 (query token, q-head) rows (128 for head_dim 256) of one request and
-// kv-head -- GQA rows packed token-major, so K/V are read once per group of
-// q-heads -- and each of the 8 wavefronts owns 2 groups of 16 rows.  Keys go
-// in 32-key steps through a three-stage LDS ring filled from registers
-// loaded three steps ahead (page ids staged in LDS, so no load waits on an
-// index load); a tile's V^T fragments are read in the step that computes its
-// scores and consumed by the next step's P.V MFMAs:
+// 256 (query token, q-head) rows of one request and kv-head -- GQA rows
+// packed token-major, so K/V are read once per group of q-heads -- and each
+// of the 8 wavefronts owns 2 groups of 16 rows.  Keys go in 32-key steps
+// through a three-stage LDS ring filled from registers loaded two steps
+// ahead (page ids staged in LDS, so no load waits on an index load); a
+// tile's V^T fragments are read in the step that computes its scores and
+// consumed by the next step's P.V MFMAs:
 //   S^T[16 keys x 16 rows] = K . Q^T    (v_mfma_f32_16x16x32, K from LDS)
 //   online softmax in fp32 (exp2 domain), causal mask aligned to the end of the KV
 //   O^T[16 dims x 16 rows] += V^T . P^T (v_mfma_f32_16x16x32, V^T from the
 //                                        transposing LDS read ds_read_b64_tr_b16)
 // The two wavefronts of each SIMD run their softmax on opposite sides of
 // their MFMA work (ping-pong), so vector and matrix work overlap.
+// At head_dim 256, prefill_rs_kernel (mi_prefill_rs.h) runs the same units
+// (128-row tiles), plan, queues, loader and LDS ring with the work split by
+// role inside each wavefront pair: one computes the scores and the softmax
+// of 32 rows, the other accumulates their P.V over all 256 dims.
 // fp8 K/V are converted to the MFMA type when a tile is stored to LDS; the
 // per-head scales multiply the scores and the output.
 #include "mi_prefill_kernel.h"
+#include "mi_prefill_rs.h"
 
 namespace mi {
 constexpr int kShortRows = kShortRowsMax;  // qo_len * group <= 16 -> decode kernel (8 on a paired plan)
@@ -271,7 +276,7 @@ static int launch_prefill(const PrefillParams& pp, int head_dim, int grid, hipSt
   switch (head_dim) {
     case 64: hipLaunchKernelGGL((prefill_kernel<MT, FP8, 64>), dim3(grid), dim3(64 * pf_waves(64)), 0, stream, pp); break;
     case 128: return prefill_d128_launch(pp, MT::kDtype == MI_F16, FP8, grid, stream);
-    case 256: hipLaunchKernelGGL((prefill_kernel<MT, FP8, 256>), dim3(grid), dim3(64 * pf_waves(256)), 0, stream, pp); break;
+    case 256: hipLaunchKernelGGL((prefill_rs_kernel<MT, FP8>), dim3(grid), dim3(512), 0, stream, pp); break;
     default: return MI_ERR_UNSUPPORTED;
   }
   return MI_OK;

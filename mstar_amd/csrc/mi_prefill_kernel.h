@@ -1,7 +1,8 @@
-// The persistent ragged prefill kernel (prefill_kernel) and its parameters,
-// shared by mi_prefill.hip (plan, launch, head_dim 64 and 256) and
+// The persistent ragged prefill kernel (prefill_kernel, head_dim 64 and 128)
+// and its parameters, shared by mi_prefill.hip (plan, launch, head_dim 64),
 // mi_prefill_d128.hip (the head_dim 128 instantiations, compiled with their
-// own scheduler setting).  The kernel's description heads mi_prefill.hip.
+// own scheduler setting) and mi_prefill_rs.h (the head_dim 256 kernel).  The
+// kernels' description heads mi_prefill.hip.
 #pragma once
 
 #include "mi_common.h"
@@ -11,13 +12,12 @@
 namespace mi {
 
 
-// Wavefronts per prefill workgroup (32 rows each): 8 (two per SIMD) while
-// the per-wave state fits 256 registers, 4 for head_dim 256.
-// Eight wavefronts (two per SIMD, in ping-pong) with two 16-row groups each;
-// head_dim 256 keeps its accumulators within a two-wavefront register share
-// with one 16-row group per wavefront.
+// Eight wavefronts per prefill workgroup (two per SIMD).  Up to head_dim 128
+// (prefill_kernel) each wavefront owns two 16-row groups: 256-row tiles.  At
+// head_dim 256 (prefill_rs_kernel, mi_prefill_rs.h) a pair of wavefronts owns
+// two 16-row groups, split by role: 128-row tiles.
 constexpr int pf_waves(int) { return 8; }
-constexpr int pf_rg(int head_dim) { return head_dim > 128 ? 1 : 2; }  // 16-row groups per wavefront
+constexpr int pf_rg(int head_dim) { return head_dim > 128 ? 1 : 2; }  // 16-row groups per wavefront (per pair at 256)
 constexpr int pf_rows(int head_dim) { return 16 * pf_rg(head_dim) * pf_waves(head_dim); }  // (token, q-head) rows per workgroup
 constexpr int kPfKeys = 32;                // keys per K/V tile
 constexpr int kPfTileCap = 1024;           // tiles whose row-group addresses are staged in LDS at a time
@@ -67,6 +67,7 @@ struct PrefillCfg {
 
 template <typename MT, bool FP8, int D>
 __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams p) {
+  static_assert(D <= 128, "head_dim 256 runs prefill_rs_kernel");
   using C = PrefillCfg<MT, FP8, D>;
   constexpr int KS = D / 32, VW = D / 16, KEYS = C::KEYS, RSK = C::RSK, RSV = C::RSV, ESZ = C::ESZ, CPR = C::CPR;
   constexpr int THREADS = C::THREADS, NL = C::NL, HALF = C::HALF, STAGE = C::STAGE;
@@ -175,9 +176,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // NB register buffers: tile X is loaded into buffer (X - t0) % NB, NB steps
   // before the step that stores it to LDS.  Two: with three (loads one step
   // further ahead) the c4 batch ran 1.5-2.5% slower at head_dim 128 (225 vs
-  // 217 VGPRs), and head_dim 256 needs the registers for its deeper LDS
-  // read-ahead (KLA, VLA below).  The step loop is unrolled over lcm(3 LDS
-  // stages, NB) steps.
+  // 217 VGPRs).  The step loop is unrolled over lcm(3 LDS stages, NB) steps.
   constexpr int NB = 2;
   constexpr int UNR = 6;
   uint4 rr[NB][NL];
@@ -293,12 +292,9 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       for (int js = 0; js < 2; ++js)
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) s[rg][js] = MT::mma_16x16x32(a[js][st], qf[rg][st], s[rg][js]);
-    // K fragment reads KLA slices ahead of the MFMAs that use them: one at
-    // head_dim 128 and below (four MFMAs per slice cover the LDS latency; c4
-    // 592 -> 586 us against all reads first), two at head_dim 256, whose
-    // slices feed two MFMAs each (with VLA: 1693 -> 1540 us on the bench's
-    // head_dim 256 batch).
-    constexpr int KLA = D > 128 ? 2 : 1;
+    // K fragment reads one slice ahead of the MFMAs that use them (four MFMAs
+    // per slice cover the LDS latency; c4 592 -> 586 us against all reads first).
+    constexpr int KLA = 1;
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * KLA, 0);
 #pragma unroll
     for (int st = KLA; st < KS; ++st) {
@@ -374,8 +370,6 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   // The fragments of tile T are read in the step that computes its scores
   // and kept in registers across the barrier: the P.V MFMAs of the next
   // step then start without waiting on LDS, while that step's K reads run.
-  // head_dim 256 (64 registers of fragments) reads them just before use.
-  constexpr bool VPRE = D <= 128;
   auto vfrag = [&](int stage, uint4 (&a)[VW]) {
     const uint8_t* vt0 = lds + stage * STAGE + KEYS * RSK + (4 * grp + ((lane & 15) >> 2)) * RSV + 8 * (lane & 3);
 #pragma unroll
@@ -391,16 +385,6 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     for (int jj = 0; jj < VW; ++jj)
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg) acc[rg][jj] = MT::mma_16x16x32(a[jj], pb[rg], acc[rg][jj]);
-    if constexpr (!VPRE) {  // fragments read just before use: VLA output tiles ahead of their MFMAs
-      constexpr int VLA = 4;
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * VLA, 0);
-#pragma unroll
-      for (int jj = VLA; jj < VW; ++jj) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, RG, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, RG * VLA, 0);
-    }
   };
   // Ping-pong: the two wavefronts that share a SIMD (one of waves {0,2,5,7},
   // one of {1,3,4,6}, for either round-robin or paired wave placement) put
@@ -442,7 +426,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
     uint4 va[VW];
     // step 0: scores and V^T fragments of tile t0; group B also its softmax
     qk(0, sc);
-    if constexpr (VPRE) vfrag(0, va);
+    vfrag(0, va);
     if (!grp_a) {
       sm_max(t0, sc);
       sm_exp(sc, pbk);
@@ -464,7 +448,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         tile_pages(min(T + 1 + NB, tl), pg4);
         // Each group's vector half runs at raised wave priority, so its softmax
         // issues ahead of the partner's MFMA stream on the shared SIMD
-        // (c4 583 -> 580 us, head_dim 256 1794 -> 1747 us).
+        // (c4 583 -> 580 us).
         if (grp_a) {
           __builtin_amdgcn_s_setprio(1);
           store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
@@ -476,9 +460,8 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         // scores of tile T first (group B's softmax waits on them), then P.V of
         // tile T-1; V^T fragments of tile T replace those of T-1 after it
         qk((u + 1) % 3, sc);       // stage of tile T = ii % 3
-        if constexpr (!VPRE) vfrag(u % 3, va);  // stage of tile T-1 = (ii-1) % 3 = u
         pv(va, pbk);               // tile T-1
-        if constexpr (VPRE) vfrag((u + 1) % 3, va);
+        vfrag((u + 1) % 3, va);
         if (!grp_a) {
           __builtin_amdgcn_s_setprio(1);
           store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
@@ -495,7 +478,6 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       sm_max(t1 - 1, sc);
       sm_exp(sc, pbk);
     }
-    if constexpr (!VPRE) vfrag((n - 1) % 3, va);
     pv(va, pbk);
   }
 

@@ -1,0 +1,426 @@
+// Role-split ragged prefill for head_dim 256 (prefill_rs_kernel).
+//
+// Same units as prefill_kernel (128-row tiles of one request and kv-head,
+// the plan's per-XCD queues), the same tile loader, page-offset table and
+// three-stage LDS ring, but the 8 wavefronts form 4 pairs, each pair owning
+// 32 rows (two 16-row groups), and the two wavefronts of a pair split the
+// work by role:
+//   S-role (waves 0, 2, 5, 7): S^T = K.Q^T for the 32 rows, the online
+//     softmax and the probabilities P(T) of tile T, written to LDS (2 KB per
+//     pair) together with each row's rescale factor;
+//   O-role (waves 1, 3, 4, 6): one step behind, O^T += V^T.P^T(T-1) over all
+//     256 dims of the 32 rows (the 128 accumulator registers an S-role
+//     wavefront uses for its Q fragments).
+// Every K and V^T fragment read from LDS then feeds two MFMAs (both 16-row
+// groups), where 16 rows per wavefront read each fragment for one: at head_dim
+// 256 those fragment reads, not the MFMAs, set the step time.  Each SIMD
+// holds one wavefront of each role for round-robin (SIMD = wave % 4) and
+// paired (SIMD = wave / 2) placement alike, so the S-role softmax runs under
+// the O-role MFMAs.
+#pragma once
+
+#include "mi_prefill_kernel.h"
+
+namespace mi {
+
+template <typename MT, bool FP8>
+__global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
+  constexpr int D = 256;
+  using C = PrefillCfg<MT, FP8, D>;
+  constexpr int KS = D / 32, VW = D / 16, KEYS = C::KEYS, RSK = C::RSK, RSV = C::RSV, ESZ = C::ESZ, CPR = C::CPR;
+  constexpr int THREADS = C::THREADS, NL = C::NL, HALF = C::HALF, STAGE = C::STAGE;
+  constexpr int LCH = FP8 ? 32 : 16;  // LDS bytes per loaded chunk
+  constexpr float kNegInf = -__builtin_inff();
+  static_assert(THREADS == 512, "four wavefront pairs");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * STAGE];
+  __shared__ int64_t lds_toff[2 * kPfTileCap];
+  // probabilities of the step (B operand layout: per pair, row group and lane
+  // one uint4) and each row's rescale factor, double-buffered by step parity
+  __shared__ uint4 lds_p[2][4][2][64];
+  __shared__ float lds_alpha[2][4][2][64];
+  __shared__ int s_unit;
+
+  const int n_tiles = p.hdr[0];
+  const int xcd = (int)blockIdx.x & 7;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = uniform(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const bool role_s = ((wave ^ (wave >> 2)) & 1) == 0;
+  const int pr = wave >> 1;  // pair: rows 32*pr .. 32*pr+31 of the tile
+  const int ps = p.page_size, G = p.group;
+
+  // Each role runs its own copy of the unit loop (the role is a compile-time
+  // constant there), so a wavefront's registers hold only its role's state:
+  // the S-role's Q fragments or the O-role's accumulators.  Both copies pass
+  // the same sequence of workgroup barriers.
+  auto run = [&](auto role) {
+    constexpr bool S = decltype(role)::value;
+    for (;;) {
+      if (tid == 0) {
+        int u = -1;
+        for (int k = 0; k < 8 && u < 0; ++k) {
+          const int y = (xcd + k) & 7;
+          const int first = p.hdr[8 + y], len = p.hdr[9 + y] - first;
+          if (len <= 0 || __hip_atomic_load(p.ctr + y * kCtrStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= len)
+            continue;
+          const int i = atomicAdd(p.ctr + y * kCtrStride, 1);
+          if (i < len) u = p.order[first + i];
+        }
+        s_unit = u;
+      }
+      __syncthreads();
+      const int unit = s_unit;
+      __syncthreads();
+      if (unit < 0) break;
+      const int h = unit / n_tiles;
+      const int2 te = p.tiles[unit - h * n_tiles];
+      const int b = te.x, row0 = te.y;
+      const int qo_start = p.qo_indptr[b];
+      const int qo_len = p.qo_indptr[b + 1] - qo_start;
+      const int page_base = p.kv_indptr[b];
+      const int np = p.kv_indptr[b + 1] - page_base;
+      const int kv_len = (np - 1) * ps + p.last_page_len[b];
+      const int rows_total = qo_len * G;
+
+      // R: the S-role's Q fragments (R[rg][s] for s < KS), the O-role's accumulators
+      f32x4 R[2][VW];
+      int lim[2];
+#pragma unroll
+      for (int rg = 0; rg < 2; ++rg) {
+        const int n = row0 + 32 * pr + 16 * rg + col;
+        const int tok = n / G, g = n - tok * G;
+        const int l = p.causal ? (kv_len - qo_len + tok) : (kv_len - 1);
+        lim[rg] = min(l, kv_len - 1);
+        if constexpr (S) {
+          const bool valid = n < rows_total;
+          const uint16_t* qrow = (const uint16_t*)p.q + (int64_t)(qo_start + tok) * p.q_stride_tok +
+                                 (int64_t)(h * G + g) * p.q_stride_head;
+#pragma unroll
+          for (int s = 0; s < KS; ++s)
+            R[rg][s] = bitcast<f32x4>(valid ? *(const uint4*)(qrow + 32 * s + 8 * grp) : make_uint4(0, 0, 0, 0));
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < VW; ++jj) R[rg][jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      const int last_row = min(row0 + C::ROWS, rows_total) - 1;
+      const int max_tok = last_row / G, min_tok = row0 / G;
+      const int kv_end = p.causal ? min(kv_len, kv_len - qo_len + max_tok + 1) : kv_len;
+      const int mask_from = p.causal ? (kv_len - qo_len + min_tok + 1) : kv_len;
+      const int n_kt = kv_end > 0 ? (kv_end + KEYS - 1) / KEYS : 0;
+
+      float kscale = 1.f, vscale = 1.f;
+      if constexpr (FP8) {
+        kscale = p.k_scale[h];
+        vscale = p.v_scale[h];
+      }
+      const float sl2 = p.scale_log2 * kscale;
+
+      // ---- loader (as prefill_kernel): chunk c = tid + i*THREADS -> (half, row, 16-byte column)
+      const uint8_t* kvb = (const uint8_t*)p.kv + (int64_t)h * p.head_stride * ESZ;
+      const int64_t tok_bytes = p.token_stride * ESZ;
+      uint32_t l_off[NL];
+      int l_grp[NL];
+      int l_row[NL];
+      bool l_v[NL];
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        const int c = tid + i * THREADS;
+        const int half = c / HALF, rem = c - half * HALF;
+        const int row = rem / CPR, ch = rem - row * CPR;
+        l_row[i] = row;
+        l_grp[i] = uniform(row) & ~15;
+        l_v[i] = half == 1;
+        l_off[i] = (uint32_t)((int64_t)half * p.kv_stride * ESZ + (int64_t)(row - (row & ~15)) * tok_bytes + 16 * ch);
+      }
+      const int key_cap = np * ps - 16;
+      const int64_t page_bytes = p.page_stride * ESZ;
+      int c0 = 0;
+      constexpr int NB = 2;
+      constexpr int UNR = 6;
+      uint4 rr[NB][NL];
+      auto tile_pages = [&](int t, int64_t (&pg)[NL]) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) pg[i] = lds_toff[2 * (t - c0) + (l_grp[i] >> 4)];
+      };
+      auto load_tile_at = [&](const int64_t (&pg)[NL], uint4 (&r)[NL]) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+          if (2 * HALF % THREADS == 0 || tid + i * THREADS < 2 * HALF) {
+            const uint8_t* base = kvb + uniform64(pg[i]);
+            r[i] = *(const uint4*)(base + l_off[i]);
+          }
+        }
+      };
+      auto load_tile = [&](int t, uint4 (&r)[NL]) {
+        int64_t pg[NL];
+        tile_pages(t, pg);
+        load_tile_at(pg, r);
+      };
+      auto store_tile_impl = [&](int t, const uint4 (&r)[NL], int stage, auto tail) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+          const int c = tid + i * THREADS;
+          if (2 * HALF % THREADS == 0 || c < 2 * HALF) {
+            const int half = c / HALF, rem = c - half * HALF;
+            const int row = rem / CPR, ch = rem - row * CPR;
+            const uint4 v = r[i];
+            uint8_t* dst = lds + stage * STAGE + (half ? KEYS * RSK + row * RSV : row * RSK) + LCH * ch;
+            if constexpr (FP8) {
+              const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+              uint32_t o[8];
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                o[2 * k] = fp8x2_to_mt<MT>(w[k], false);
+                o[2 * k + 1] = fp8x2_to_mt<MT>(w[k], true);
+              }
+              *(uint4*)dst = make_uint4(o[0], o[1], o[2], o[3]);
+              *(uint4*)(dst + 16) = make_uint4(o[4], o[5], o[6], o[7]);
+            } else {
+              *(uint4*)dst = v;
+            }
+            if constexpr (decltype(tail)::value) {
+              if (l_v[i] && t * KEYS + l_row[i] >= kv_len) {
+                *(uint4*)dst = make_uint4(0, 0, 0, 0);
+                if constexpr (FP8) *(uint4*)(dst + 16) = make_uint4(0, 0, 0, 0);
+              }
+            }
+          }
+        }
+      };
+      auto store_tile = [&](int t, const uint4 (&r)[NL], int stage) {
+        if (t * KEYS + KEYS > kv_len)
+          store_tile_impl(t, r, stage, std::true_type{});
+        else
+          store_tile_impl(t, r, stage, std::false_type{});
+      };
+
+      // S-role softmax state (lazy running max, as prefill_kernel)
+      constexpr float kLazy = 8.f;
+      const float lazy_raw = kLazy / sl2;
+      float m_run[2], l_run[2], thr[2], moff[2];
+#pragma unroll
+      for (int rg = 0; rg < 2; ++rg) {
+        m_run[rg] = kNegInf;
+        l_run[rg] = 0.f;
+        thr[rg] = kNegInf;
+        moff[rg] = 0.f;
+      }
+      const int t_mask = mask_from > 0 ? mask_from / KEYS : 0;
+
+      // S-role: scores, softmax and probabilities of tile t (K in LDS stage
+      // `stage`), published in the exchange buffers of parity t & 1.
+      auto s_step = [&](int t, int stage) {
+        const uint8_t* sk = lds + stage * STAGE;
+        f32x4 s[2][2];
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+          for (int js = 0; js < 2; ++js) s[rg][js] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // K fragments in chunks of KC 32-dim slices (both 16-key halves), one
+        // chunk read ahead of its MFMAs; the empty asm with a memory clobber
+        // keeps the compiler from hoisting every read (64 registers).
+        constexpr int KC = 2;
+        uint4 ka[2][KC][2];
+        auto kread = [&](int c, uint4 (&a)[KC][2]) {
+#pragma unroll
+          for (int k = 0; k < KC; ++k)
+#pragma unroll
+            for (int js = 0; js < 2; ++js)
+              a[k][js] = *(const uint4*)(sk + (16 * js + col) * RSK + (8 * grp + 32 * (KC * c + k)) * 2);
+        };
+        kread(0, ka[0]);
+#pragma unroll
+        for (int c = 0; c < KS / KC; ++c) {
+          if (c + 1 < KS / KC) kread(c + 1, ka[(c + 1) & 1]);
+          asm volatile("" ::: "memory");
+#pragma unroll
+          for (int k = 0; k < KC; ++k)
+#pragma unroll
+            for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+              for (int js = 0; js < 2; ++js)
+                s[rg][js] = MT::mma_16x16x32(ka[c & 1][k][js], bitcast<uint4>(R[rg][KC * c + k]), s[rg][js]);
+        }
+        const int kb = t * KEYS;
+        if (t >= t_mask) {
+#pragma unroll
+          for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+            for (int js = 0; js < 2; ++js)
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (kb + 16 * js + 4 * grp + r > lim[rg]) s[rg][js][r] = kNegInf;
+        }
+        float ml[2], alpha[2] = {1.f, 1.f};
+        bool any_need = false;
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+          float m = kNegInf;
+#pragma unroll
+          for (int js = 0; js < 2; ++js)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) m = fmaxf(m, s[rg][js][r]);
+          ml[rg] = m;
+          any_need |= m > thr[rg];
+        }
+        if (__builtin_amdgcn_ballot_w64(any_need)) {
+#pragma unroll
+          for (int rg = 0; rg < 2; ++rg) {
+            const float mt = rows4_max(ml[rg]);
+            const bool grow = mt > thr[rg];
+            alpha[rg] = grow ? fast_exp2((m_run[rg] - mt) * sl2) : 1.f;
+            if (grow) {
+              m_run[rg] = mt;
+              thr[rg] = mt + lazy_raw;
+              moff[rg] = mt == kNegInf ? 0.f : -mt * sl2;
+            }
+          }
+        }
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+          float q[2][4];
+#pragma unroll
+          for (int js = 0; js < 2; ++js)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) q[js][r] = fast_exp2(fmaf(s[rg][js][r], sl2, moff[rg]));
+          const uint4 pb = make_uint4(MT::pack2(q[0][0], q[0][1]), MT::pack2(q[0][2], q[0][3]),
+                                      MT::pack2(q[1][0], q[1][1]), MT::pack2(q[1][2], q[1][3]));
+          lds_p[t & 1][pr][rg][lane] = pb;
+          lds_alpha[t & 1][pr][rg][lane] = alpha[rg];
+        }
+      };
+      // O-role: O^T += V^T.P^T of tile t (V in LDS stage `stage`), after the
+      // rescale the S-role found for that tile.
+      auto o_step = [&](int t, int stage) {
+        uint4 pb[2];
+        float alpha[2];
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+          pb[rg] = lds_p[t & 1][pr][rg][lane];
+          alpha[rg] = lds_alpha[t & 1][pr][rg][lane];
+        }
+        if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f)) {
+#pragma unroll
+          for (int rg = 0; rg < 2; ++rg)
+#pragma unroll
+            for (int jj = 0; jj < VW; ++jj) R[rg][jj] *= alpha[rg];
+#pragma unroll
+          for (int rg = 0; rg < 2; ++rg) l_run[rg] *= alpha[rg];
+        }
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg)
+          l_run[rg] = MT::sum2(pb[rg].w, MT::sum2(pb[rg].z, MT::sum2(pb[rg].y, MT::sum2(pb[rg].x, l_run[rg]))));
+        const uint8_t* vt0 = lds + stage * STAGE + KEYS * RSK + (4 * grp + ((lane & 15) >> 2)) * RSV + 8 * (lane & 3);
+        // V^T fragments in chunks of VC output tiles, one chunk read ahead of
+        // the MFMAs that use it: the empty asm with a memory clobber keeps the
+        // compiler from hoisting every read (64 registers) above the MFMAs.
+        constexpr int VC = 4;
+        uint4 va[2][VC];
+        auto vread = [&](int c, uint4 (&a)[VC]) {
+#pragma unroll
+          for (int k = 0; k < VC; ++k) {
+            const int jj = VC * c + k;
+            const v4i16 x0 = ds_read_tr16(vt0 + 32 * jj);
+            const v4i16 x1 = ds_read_tr16(vt0 + 16 * RSV + 32 * jj);
+            const uint2 a0 = bitcast<uint2>(x0), a1 = bitcast<uint2>(x1);
+            a[k] = make_uint4(a0.x, a0.y, a1.x, a1.y);
+          }
+        };
+        vread(0, va[0]);
+#pragma unroll
+        for (int c = 0; c < VW / VC; ++c) {
+          if (c + 1 < VW / VC) vread(c + 1, va[(c + 1) & 1]);
+          asm volatile("" ::: "memory");
+#pragma unroll
+          for (int k = 0; k < VC; ++k)
+#pragma unroll
+            for (int rg = 0; rg < 2; ++rg)
+              R[rg][VC * c + k] = MT::mma_16x16x32(va[c & 1][k], pb[rg], R[rg][VC * c + k]);
+        }
+      };
+
+      // ---- tile chunks, as prefill_kernel: step T stores tile T+1 into the
+      // stage tile T-2 used and loads tile T+1+NB; the S-role reads K of tile T,
+      // the O-role V of tile T-1.
+      for (c0 = 0; c0 * KEYS < kv_end; c0 += kPfTileCap) {
+        const int t0 = c0;
+        const int t1 = min(n_kt, c0 + kPfTileCap);
+        __syncthreads();
+        for (int e = tid; e < 2 * (t1 - t0); e += THREADS) {
+          const int key = min((t0 + (e >> 1)) * KEYS + 16 * (e & 1), key_cap);
+          const int pidx = (int)((unsigned)key / (unsigned)ps);
+          const int slot = key - pidx * ps;
+          lds_toff[e] = (int64_t)p.kv_indices[page_base + pidx] * page_bytes + (int64_t)slot * tok_bytes;
+        }
+        __syncthreads();
+        const int tl = t1 - 1;
+        const int n = t1 - t0;
+#pragma unroll
+        for (int u = 0; u < NB; ++u) load_tile(min(t0 + u, tl), rr[u]);
+        store_tile(t0, rr[0], 0);
+        load_tile(min(t0 + NB, tl), rr[0]);
+        __syncthreads();
+        // step 0: scores of tile t0
+        if constexpr (S) s_step(t0, 0);
+        store_tile(min(t0 + 1, tl), rr[1 % NB], 1);
+        load_tile(min(t0 + 1 + NB, tl), rr[1 % NB]);
+        __syncthreads();
+        for (int i = 1; i < n; i += UNR) {
+#pragma unroll
+          for (int u = 0; u < UNR; ++u) {
+            const int ii = i + u;
+            if (ii >= n) break;
+            const int T = t0 + ii;
+            if constexpr (S) {
+              s_step(T, (u + 1) % 3);  // stage of tile T = ii % 3
+              store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
+              load_tile(min(T + 1 + NB, tl), rr[(u + 2) % NB]);
+            } else {
+              store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
+              load_tile(min(T + 1 + NB, tl), rr[(u + 2) % NB]);
+              o_step(T - 1, u % 3);  // stage of tile T-1 = (ii-1) % 3
+            }
+            __syncthreads();
+          }
+        }
+        // last step: P.V of tile t1-1
+        if constexpr (!S) o_step(t1 - 1, (n - 1) % 3);
+      }
+
+      // ---- epilogue: the S-role publishes its row sums, the O-role writes the rows
+      if constexpr (!S) {
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+          const float l_tot = rows4_sum(l_run[rg]);
+          const float inv = l_tot > 0.f ? vscale / l_tot : (l_tot == 0.f ? 0.f : __builtin_nanf(""));
+          const int nrow = row0 + 32 * pr + 16 * rg + col;
+          if (nrow >= rows_total) continue;
+          const int tok = nrow / G, g = nrow - tok * G;
+          uint16_t* orow = (uint16_t*)p.out + (int64_t)(qo_start + tok) * p.out_stride_tok +
+                           (int64_t)(h * G + g) * p.out_stride_head;
+#pragma unroll
+          for (int jj = 0; jj < VW; ++jj) {
+            const f32x4 o = R[rg][jj];
+            *(uint2*)(orow + 16 * jj + 4 * grp) =
+                make_uint2(MT::pack2(o[0] * inv, o[1] * inv), MT::pack2(o[2] * inv, o[3] * inv));
+          }
+        }
+      }
+    }  // unit loop
+  };
+  if (role_s)
+    run(std::true_type{});
+  else
+    run(std::false_type{});
+  if (tid == 0) {
+    __threadfence();
+    if (atomicAdd(p.ctr + 8 * kCtrStride, 1) == (int)gridDim.x - 1) {
+#pragma unroll
+      for (int y = 0; y < 9; ++y) __hip_atomic_store(p.ctr + y * kCtrStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+}  // namespace mi
