@@ -276,7 +276,7 @@ static int launch_prefill(const PrefillParams& pp, int head_dim, int grid, hipSt
   switch (head_dim) {
     case 64: hipLaunchKernelGGL((prefill_kernel<MT, FP8, 64>), dim3(grid), dim3(64 * pf_waves(64)), 0, stream, pp); break;
     case 128: return prefill_d128_launch(pp, MT::kDtype == MI_F16, FP8, grid, stream);
-    case 256: hipLaunchKernelGGL((prefill_rs_kernel<MT, FP8>), dim3(grid), dim3(512), 0, stream, pp); break;
+    case 256: hipLaunchKernelGGL((prefill_rs_kernel<MT, FP8, 256>), dim3(grid), dim3(512), 0, stream, pp); break;
     default: return MI_ERR_UNSUPPORTED;
   }
   return MI_OK;

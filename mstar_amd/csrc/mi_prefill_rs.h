@@ -23,10 +23,13 @@
 
 namespace mi {
 
-template <typename MT, bool FP8>
+template <typename MT, bool FP8, int D>
 __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
-  constexpr int D = 256;
   using C = PrefillCfg<MT, FP8, D>;
+  // 16-row groups per pair: the O-role's accumulators (RGP x D/16 f32x4) fill
+  // 128 registers at either head_dim; C::ROWS = 4 pairs x 16 x RGP
+  constexpr int RGP = D > 128 ? 2 : 4, PROWS = 16 * RGP;
+  static_assert(C::ROWS == 4 * PROWS, "tile rows = four pairs");
   constexpr int KS = D / 32, VW = D / 16, KEYS = C::KEYS, RSK = C::RSK, RSV = C::RSV, ESZ = C::ESZ, CPR = C::CPR;
   constexpr int THREADS = C::THREADS, NL = C::NL, HALF = C::HALF, STAGE = C::STAGE;
   constexpr int LCH = FP8 ? 32 : 16;  // LDS bytes per loaded chunk
@@ -36,8 +39,8 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
   __shared__ int64_t lds_toff[2 * kPfTileCap];
   // probabilities of the step (B operand layout: per pair, row group and lane
   // one uint4) and each row's rescale factor, double-buffered by step parity
-  __shared__ uint4 lds_p[2][4][2][64];
-  __shared__ float lds_alpha[2][4][2][64];
+  __shared__ uint4 lds_p[2][4][RGP][64];
+  __shared__ float lds_alpha[2][4][RGP][64];
   __shared__ int s_unit;
 
   const int n_tiles = p.hdr[0];
@@ -84,11 +87,11 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
       const int rows_total = qo_len * G;
 
       // R: the S-role's Q fragments (R[rg][s] for s < KS), the O-role's accumulators
-      f32x4 R[2][VW];
-      int lim[2];
+      f32x4 R[RGP][VW];
+      int lim[RGP];
 #pragma unroll
-      for (int rg = 0; rg < 2; ++rg) {
-        const int n = row0 + 32 * pr + 16 * rg + col;
+      for (int rg = 0; rg < RGP; ++rg) {
+        const int n = row0 + PROWS * pr + 16 * rg + col;
         const int tok = n / G, g = n - tok * G;
         const int l = p.causal ? (kv_len - qo_len + tok) : (kv_len - 1);
         lim[rg] = min(l, kv_len - 1);
@@ -199,9 +202,9 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
       // S-role softmax state (lazy running max, as prefill_kernel)
       constexpr float kLazy = 8.f;
       const float lazy_raw = kLazy / sl2;
-      float m_run[2], l_run[2], thr[2], moff[2];
+      float m_run[RGP], l_run[RGP], thr[RGP], moff[RGP];
 #pragma unroll
-      for (int rg = 0; rg < 2; ++rg) {
+      for (int rg = 0; rg < RGP; ++rg) {
         m_run[rg] = kNegInf;
         l_run[rg] = 0.f;
         thr[rg] = kNegInf;
@@ -213,9 +216,9 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
       // `stage`), published in the exchange buffers of parity t & 1.
       auto s_step = [&](int t, int stage) {
         const uint8_t* sk = lds + stage * STAGE;
-        f32x4 s[2][2];
+        f32x4 s[RGP][2];
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg)
+        for (int rg = 0; rg < RGP; ++rg)
 #pragma unroll
           for (int js = 0; js < 2; ++js) s[rg][js] = f32x4{0.f, 0.f, 0.f, 0.f};
         // K fragments in chunks of KC 32-dim slices (both 16-key halves), one
@@ -238,7 +241,7 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
 #pragma unroll
           for (int k = 0; k < KC; ++k)
 #pragma unroll
-            for (int rg = 0; rg < 2; ++rg)
+            for (int rg = 0; rg < RGP; ++rg)
 #pragma unroll
               for (int js = 0; js < 2; ++js)
                 s[rg][js] = MT::mma_16x16x32(ka[c & 1][k][js], bitcast<uint4>(R[rg][KC * c + k]), s[rg][js]);
@@ -246,17 +249,19 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
         const int kb = t * KEYS;
         if (t >= t_mask) {
 #pragma unroll
-          for (int rg = 0; rg < 2; ++rg)
+          for (int rg = 0; rg < RGP; ++rg)
 #pragma unroll
             for (int js = 0; js < 2; ++js)
 #pragma unroll
               for (int r = 0; r < 4; ++r)
                 if (kb + 16 * js + 4 * grp + r > lim[rg]) s[rg][js][r] = kNegInf;
         }
-        float ml[2], alpha[2] = {1.f, 1.f};
+        float ml[RGP], alpha[RGP];
+#pragma unroll
+        for (int rg = 0; rg < RGP; ++rg) alpha[rg] = 1.f;
         bool any_need = false;
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
+        for (int rg = 0; rg < RGP; ++rg) {
           float m = kNegInf;
 #pragma unroll
           for (int js = 0; js < 2; ++js)
@@ -267,7 +272,7 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
         }
         if (__builtin_amdgcn_ballot_w64(any_need)) {
 #pragma unroll
-          for (int rg = 0; rg < 2; ++rg) {
+          for (int rg = 0; rg < RGP; ++rg) {
             const float mt = rows4_max(ml[rg]);
             const bool grow = mt > thr[rg];
             alpha[rg] = grow ? fast_exp2((m_run[rg] - mt) * sl2) : 1.f;
@@ -279,7 +284,7 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
           }
         }
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
+        for (int rg = 0; rg < RGP; ++rg) {
           float q[2][4];
 #pragma unroll
           for (int js = 0; js < 2; ++js)
@@ -294,23 +299,26 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
       // O-role: O^T += V^T.P^T of tile t (V in LDS stage `stage`), after the
       // rescale the S-role found for that tile.
       auto o_step = [&](int t, int stage) {
-        uint4 pb[2];
-        float alpha[2];
+        uint4 pb[RGP];
+        float alpha[RGP];
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
+        for (int rg = 0; rg < RGP; ++rg) {
           pb[rg] = lds_p[t & 1][pr][rg][lane];
           alpha[rg] = lds_alpha[t & 1][pr][rg][lane];
         }
-        if (__builtin_amdgcn_ballot_w64(alpha[0] != 1.f || alpha[1] != 1.f)) {
+        bool rescale = false;
 #pragma unroll
-          for (int rg = 0; rg < 2; ++rg)
+        for (int rg = 0; rg < RGP; ++rg) rescale |= alpha[rg] != 1.f;
+        if (__builtin_amdgcn_ballot_w64(rescale)) {
+#pragma unroll
+          for (int rg = 0; rg < RGP; ++rg)
 #pragma unroll
             for (int jj = 0; jj < VW; ++jj) R[rg][jj] *= alpha[rg];
 #pragma unroll
-          for (int rg = 0; rg < 2; ++rg) l_run[rg] *= alpha[rg];
+          for (int rg = 0; rg < RGP; ++rg) l_run[rg] *= alpha[rg];
         }
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg)
+        for (int rg = 0; rg < RGP; ++rg)
           l_run[rg] = MT::sum2(pb[rg].w, MT::sum2(pb[rg].z, MT::sum2(pb[rg].y, MT::sum2(pb[rg].x, l_run[rg]))));
         const uint8_t* vt0 = lds + stage * STAGE + KEYS * RSK + (4 * grp + ((lane & 15) >> 2)) * RSV + 8 * (lane & 3);
         // V^T fragments in chunks of VC output tiles, one chunk read ahead of
@@ -336,7 +344,7 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
 #pragma unroll
           for (int k = 0; k < VC; ++k)
 #pragma unroll
-            for (int rg = 0; rg < 2; ++rg)
+            for (int rg = 0; rg < RGP; ++rg)
               R[rg][VC * c + k] = MT::mma_16x16x32(va[c & 1][k], pb[rg], R[rg][VC * c + k]);
         }
       };
@@ -392,10 +400,10 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
       // ---- epilogue: the S-role publishes its row sums, the O-role writes the rows
       if constexpr (!S) {
 #pragma unroll
-        for (int rg = 0; rg < 2; ++rg) {
+        for (int rg = 0; rg < RGP; ++rg) {
           const float l_tot = rows4_sum(l_run[rg]);
           const float inv = l_tot > 0.f ? vscale / l_tot : (l_tot == 0.f ? 0.f : __builtin_nanf(""));
-          const int nrow = row0 + 32 * pr + 16 * rg + col;
+          const int nrow = row0 + PROWS * pr + 16 * rg + col;
           if (nrow >= rows_total) continue;
           const int tok = nrow / G, g = nrow - tok * G;
           uint16_t* orow = (uint16_t*)p.out + (int64_t)(qo_start + tok) * p.out_stride_tok +
