@@ -31,7 +31,7 @@ from mstar_amd.paged_attention import FlashInferPrefillWrapper
 
 pytestmark = pytest.mark.gpu
 
-HQ, HKV, D, PS, LAYERS, SEQ = 28, 4, 128, 16, 2, 64
+PS, LAYERS, SEQ = 16, 2, 64
 
 
 def _schedule(bs):
@@ -55,8 +55,9 @@ def _schedule(bs):
     return out
 
 
-@pytest.mark.parametrize("BS", [4, 130])
-def test_packed_prefill_graph_replays_with_padding(gpu, BS):
+# c4's heads (head_dim 128, the ping-pong tiles) and the Pi0.5 heads (head_dim 256, the role-split tiles)
+@pytest.mark.parametrize("BS,HQ,HKV,D", [(4, 28, 4, 128), (130, 28, 4, 128), (4, 8, 1, 256)])
+def test_packed_prefill_graph_replays_with_padding(gpu, BS, HQ, HKV, D):
     POOL = 512 if BS == 4 else 4096
     cfg = KVCacheConfig(num_layers=LAYERS, num_kv_heads=HKV, head_dim=D, max_seq_len=4096, max_num_pages=POOL,
                         page_size=PS, num_qo_heads=HQ)
@@ -98,7 +99,8 @@ def test_packed_prefill_graph_replays_with_padding(gpu, BS):
         mgr.add_request(r, ["main"])
     from mstar_amd import _lib
 
-    log(f"BS={BS}: short-query threshold {_lib.lib().mi_prefill_short_rows(BS, HQ, HKV, D)} rows")
+    short = _lib.lib().mi_prefill_short_rows(BS, HQ, HKV, D)
+    log(f"BS={BS} heads {HQ}/{HKV} D={D}: short-query threshold {short} rows")
     for step, (live, new) in enumerate(_schedule(BS)):
         ids = live + dummies[len(live):]
         sls = new + [0] * (BS - len(live))
