@@ -1,22 +1,23 @@
-// Role-split ragged prefill for head_dim 256 (prefill_rs_kernel).
+// Role-split ragged prefill (prefill_rs_kernel), the head_dim 256 kernel.
 //
-// Same units as prefill_kernel (128-row tiles of one request and kv-head,
-// the plan's per-XCD queues), the same tile loader, page-offset table and
-// three-stage LDS ring, but the 8 wavefronts form 4 pairs, each pair owning
-// 32 rows (two 16-row groups), and the two wavefronts of a pair split the
-// work by role:
-//   S-role (waves 0, 2, 5, 7): S^T = K.Q^T for the 32 rows, the online
+// Same units as prefill_kernel (128-row tiles of one request and kv-head at
+// head_dim 256, the plan's per-XCD queues), the same tile loader, page-offset
+// table and three-stage LDS ring, but the 8 wavefronts form 4 pairs, each pair
+// owning PROWS rows (RGP 16-row groups: 32 rows at head_dim 256), and the two
+// wavefronts of a pair split the work by role:
+//   S-role (waves 0, 2, 5, 7): S^T = K.Q^T for the pair's rows, the online
 //     softmax and the probabilities P(T) of tile T, written to LDS (2 KB per
-//     pair) together with each row's rescale factor;
+//     pair at head_dim 256) together with each row's rescale factor;
 //   O-role (waves 1, 3, 4, 6): one step behind, O^T += V^T.P^T(T-1) over all
-//     256 dims of the 32 rows (the 128 accumulator registers an S-role
-//     wavefront uses for its Q fragments).
-// Every K and V^T fragment read from LDS then feeds two MFMAs (both 16-row
-// groups), where 16 rows per wavefront read each fragment for one: at head_dim
-// 256 those fragment reads, not the MFMAs, set the step time.  Each SIMD
-// holds one wavefront of each role for round-robin (SIMD = wave % 4) and
-// paired (SIMD = wave / 2) placement alike, so the S-role softmax runs under
-// the O-role MFMAs.
+//     dims of the pair's rows, and the rows' probability sums (the 128
+//     accumulator registers hold what an S-role wavefront holds as Q).
+// Every K and V^T fragment read from LDS then feeds RGP MFMAs, where 16 rows
+// per wavefront read each fragment for one: at head_dim 256 those fragment
+// reads, not the MFMAs, set the step time.  Each SIMD holds one wavefront of
+// each role for round-robin (SIMD = wave % 4) and paired (SIMD = wave / 2)
+// placement alike, so the S-role softmax runs under the O-role MFMAs.  The
+// template also builds at head_dim 128 (pairs of 64 rows, four row groups),
+// which measured slower than prefill_kernel there and is not launched.
 #pragma once
 
 #include "mi_prefill_kernel.h"
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
   const int wave = uniform(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const bool role_s = ((wave ^ (wave >> 2)) & 1) == 0;
-  const int pr = wave >> 1;  // pair: rows 32*pr .. 32*pr+31 of the tile
+  const int pr = wave >> 1;  // pair: rows PROWS*pr .. PROWS*(pr+1)-1 of the tile
   const int ps = p.page_size, G = p.group;
 
   // Each role runs its own copy of the unit loop (the role is a compile-time
@@ -199,7 +200,8 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
           store_tile_impl(t, r, stage, std::false_type{});
       };
 
-      // S-role softmax state (lazy running max, as prefill_kernel)
+      // softmax state: the S-role's lazy running max (as prefill_kernel), the
+      // O-role's row sums of the probabilities it accumulates
       constexpr float kLazy = 8.f;
       const float lazy_raw = kLazy / sl2;
       float m_run[RGP], l_run[RGP], thr[RGP], moff[RGP];
