@@ -123,12 +123,12 @@ def _poison_tails(cache_cpu, kv_indptr, kv_indices, last, dtype):
 
 
 def _fp8_cache(src):
-    pool = src.shape[0]
-    ks = A.head_scales(src[:, 0].reshape(-1, HKV, D))
-    vs = A.head_scales(src[:, 1].reshape(-1, HKV, D))
-    c = torch.empty(pool, 2, PS, HKV, D, dtype=torch.float8_e4m3fn)
-    c[:, 0] = A.quantize_e4m3(src[:, 0].reshape(-1, HKV, D), ks).view(pool, PS, HKV, D)
-    c[:, 1] = A.quantize_e4m3(src[:, 1].reshape(-1, HKV, D), vs).view(pool, PS, HKV, D)
+    pool, _, ps, hkv, d = src.shape
+    ks = A.head_scales(src[:, 0].reshape(-1, hkv, d))
+    vs = A.head_scales(src[:, 1].reshape(-1, hkv, d))
+    c = torch.empty(pool, 2, ps, hkv, d, dtype=torch.float8_e4m3fn)
+    c[:, 0] = A.quantize_e4m3(src[:, 0].reshape(-1, hkv, d), ks).view(pool, ps, hkv, d)
+    c[:, 1] = A.quantize_e4m3(src[:, 1].reshape(-1, hkv, d), vs).view(pool, ps, hkv, d)
     return c, (ks, vs)
 
 
@@ -162,21 +162,25 @@ def test_decode_ignores_slots_past_kv_len(gpu, batch, dtype):
     log(f"decode B={batch} {dtype}: {n} tail elements NaN/Inf, output bit-identical")
 
 
-@pytest.mark.parametrize("dtype,causal", [(torch.bfloat16, True), (torch.bfloat16, False),
-                                          (torch.float8_e4m3fn, True), (torch.float32, True)])
-def test_prefill_ignores_slots_past_kv_len(gpu, dtype, causal):
-    """A ragged batch: long chunks (MFMA tiles), short queries (decode kernel
-    with qo_indptr) and single tokens; its appended tokens end mid-page."""
+@pytest.mark.parametrize("dtype,causal,hq,hkv,d", [(torch.bfloat16, True, HQ, HKV, D), (torch.bfloat16, False, HQ, HKV, D),
+                                                   (torch.float8_e4m3fn, True, HQ, HKV, D),
+                                                   (torch.float32, True, HQ, HKV, D),
+                                                   (torch.bfloat16, True, 8, 1, 256), (torch.bfloat16, False, 8, 1, 256),
+                                                   (torch.float8_e4m3fn, True, 8, 1, 256)])
+def test_prefill_ignores_slots_past_kv_len(gpu, dtype, causal, hq, hkv, d):
+    """A ragged batch: long chunks (MFMA tiles; head_dim 256: the role-split
+    tiles), short queries (decode kernel with qo_indptr) and single tokens;
+    its appended tokens end mid-page."""
     kv_lens = [700, 1301, 33, 5, 250, 17, 900]
     new_lens = [300, 645, 2, 1, 250, 1, 9]
     qo, kv_indptr, kv_indices, last, pool = _batch(kv_lens, seed=31, new_lens=new_lens)
     g = torch.Generator().manual_seed(32)
-    src = random_cache(pool, PS, HKV, D, 33, torch.float32)
+    src = random_cache(pool, PS, hkv, d, 33, torch.float32)
     qdt = torch.bfloat16 if dtype == torch.float8_e4m3fn else dtype
     ntok = int(qo[-1])
-    q = torch.randn(ntok, HQ, D, generator=g).to(qdt)
-    k = torch.randn(ntok, HKV, D, generator=g).to(qdt)
-    v = torch.randn(ntok, HKV, D, generator=g).to(qdt)
+    q = torch.randn(ntok, hq, d, generator=g).to(qdt)
+    k = torch.randn(ntok, hkv, d, generator=g).to(qdt)
+    v = torch.randn(ntok, hkv, d, generator=g).to(qdt)
     if dtype == torch.float8_e4m3fn:
         finite, scales = _fp8_cache(src)
     else:
@@ -186,7 +190,7 @@ def test_prefill_ignores_slots_past_kv_len(gpu, dtype, causal):
     outs = []
     for c in (finite, poisoned):
         cache = c.to(gpu)
-        w = FlashInferPrefillWrapper(workspace(gpu, 64 << 20), HQ, HKV, D, PS, device=gpu)
+        w = FlashInferPrefillWrapper(workspace(gpu, 64 << 20), hq, hkv, d, PS, device=gpu)
         w.plan(torch.as_tensor(qo), torch.as_tensor(kv_indptr), torch.as_tensor(kv_indices), torch.as_tensor(last),
                causal=causal, dtype=qdt)
         sc = tuple(s.to(gpu) if s is not None else None for s in scales)
@@ -196,4 +200,4 @@ def test_prefill_ignores_slots_past_kv_len(gpu, dtype, causal):
     a, b = outs
     assert torch.isfinite(a.float()).all()
     assert torch.equal(a.view(INT_OF[a.dtype]), b.view(INT_OF[b.dtype])), "non-finite tail slots changed the output"
-    log(f"prefill {dtype} causal={causal}: {n} tail elements NaN/Inf, output bit-identical")
+    log(f"prefill {dtype} causal={causal} heads {hq}/{hkv} d={d}: {n} tail elements NaN/Inf, output bit-identical")
