@@ -1,10 +1,10 @@
 // Role-split ragged prefill (prefill_rs_kernel), the head_dim 256 kernel.
 //
 // Same units as prefill_kernel (128-row tiles of one request and kv-head at
-// head_dim 256, the plan's per-XCD queues), the same tile loader, page-offset
-// table and three-stage LDS ring, but the 8 wavefronts form 4 pairs, each pair
-// owning PROWS rows (RGP 16-row groups: 32 rows at head_dim 256), and the two
-// wavefronts of a pair split the work by role:
+// head_dim 256, the plan's per-XCD queues) and page-offset table, but the 8
+// wavefronts form 4 pairs, each pair owning PROWS rows (RGP 16-row groups: 32
+// rows at head_dim 256), and the two wavefronts of a pair split the work by
+// role:
 //   S-role (waves 0, 2, 5, 7): S^T = K.Q^T for the pair's rows, the online
 //     softmax and the probabilities P(T) of tile T, written to LDS (2 KB per
 //     pair at head_dim 256) together with each row's rescale factor;
@@ -15,9 +15,14 @@
 // per wavefront read each fragment for one: at head_dim 256 those fragment
 // reads, not the MFMAs, set the step time.  Each SIMD holds one wavefront of
 // each role for round-robin (SIMD = wave % 4) and paired (SIMD = wave / 2)
-// placement alike, so the S-role softmax runs under the O-role MFMAs.  The
-// template also builds at head_dim 128 (pairs of 64 rows, four row groups),
-// which measured slower than prefill_kernel there and is not launched.
+// placement alike, so the S-role softmax runs under the O-role MFMAs.
+// Tiles of a 16-bit cache go from memory straight into LDS (global_load_lds,
+// 16 bytes per lane, issued at the end of step T for tile T+2): the tile bytes
+// then pass through no registers and no ds_write, which had cost ~16% of the
+// kernel's cycles.  fp8 tiles are widened in registers on the way, as in
+// prefill_kernel.  The fp8 path also builds at head_dim 128 (pairs of 64 rows,
+// four row groups), which measured slower than prefill_kernel there and is not
+// launched.
 #pragma once
 
 #include "mi_prefill_kernel.h"
@@ -36,8 +41,19 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
   constexpr int LCH = FP8 ? 32 : 16;  // LDS bytes per loaded chunk
   constexpr float kNegInf = -__builtin_inff();
   static_assert(THREADS == 512, "four wavefront pairs");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * STAGE];
-  __shared__ int64_t lds_toff[2 * kPfTileCap];
+  static_assert(RSK == RSV, "one LDS row stride for K and V");
+  // 16-bit caches: direct loads into 4-stage K and V rings of unpadded rows
+  // whose 16-byte chunks are XOR-swizzled (K: chunk ^ (row & 15); V: 32-byte
+  // segment ^ (row & 7)), so the fragment reads stay free of bank conflicts;
+  // the page-offset table holds half as many tiles to leave LDS for the rings.
+  // fp8 caches: a 3-stage ring of padded rows, stored from registers.
+  constexpr bool DMA = !FP8;
+  constexpr int RS = DMA ? D * 2 : RSK;  // LDS row stride
+  constexpr int KSZ = KEYS * RS, VSZ = KEYS * RS, NKS = DMA ? 4 : 3, NVS = DMA ? 4 : 3, VOFF = NKS * KSZ;
+  constexpr int CAP = DMA ? kPfTileCap / 2 : kPfTileCap;  // tiles whose page offsets are staged at a time
+  static_assert(!DMA || (KEYS == 32 && D * 2 == 512 && THREADS == 512), "direct loads: 4 per thread and tile");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[NKS * KSZ + NVS * VSZ];
+  __shared__ int64_t lds_toff[2 * CAP];
   // probabilities of the step (B operand layout: per pair, row group and lane
   // one uint4) and each row's rescale factor, double-buffered by step parity
   __shared__ uint4 lds_p[2][4][RGP][64];
@@ -170,7 +186,7 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
             const int half = c / HALF, rem = c - half * HALF;
             const int row = rem / CPR, ch = rem - row * CPR;
             const uint4 v = r[i];
-            uint8_t* dst = lds + stage * STAGE + (half ? KEYS * RSK + row * RSV : row * RSK) + LCH * ch;
+            uint8_t* dst = lds + (half ? VOFF + stage * VSZ : stage * KSZ) + row * RS + LCH * ch;
             if constexpr (FP8) {
               const uint32_t w[4] = {v.x, v.y, v.z, v.w};
               uint32_t o[8];
@@ -199,6 +215,52 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
         else
           store_tile_impl(t, r, stage, std::false_type{});
       };
+      // Direct loads: load i of wave w fills rows 2*rp, 2*rp+1 (rp = 8*(i&1) + w,
+      // both in 16-row group i&1) of the tile's K (i < 2) or V (i >= 2) half;
+      // lane l writes LDS chunk l%32 of row 2*rp + l/32 with the cached chunk
+      // the swizzle puts there.
+      uint32_t d_off[4];
+      if constexpr (DMA) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int hv = i >> 1, rp = 8 * (i & 1) + wave, r = 2 * rp + (lane >> 5), pch = lane & 31;
+          const int c = hv ? (pch ^ (2 * (r & 7))) : (pch ^ (r & 15));
+          d_off[i] = (uint32_t)((int64_t)hv * p.kv_stride * ESZ + (int64_t)(r & 15) * tok_bytes + 16 * c);
+        }
+      }
+      const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+      auto dma_tile = [&](int t, int kst, int vst) {
+        // both 16-row groups' page offsets first, then the four loads (scalar
+        // base + 32-bit lane offset)
+        const uint8_t* gb[2] = {kvb + uniform64(lds_toff[2 * (t - c0)]), kvb + uniform64(lds_toff[2 * (t - c0) + 1])};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rp = 8 * (i & 1) + wave;
+          const uint32_t m0 = lds_base + (i >= 2 ? VOFF + vst * VSZ : kst * KSZ) + rp * 1024;
+          asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(d_off[i]), "s"(gb[i & 1])
+                       : "memory", "m0");
+        }
+      };
+      // End of a step: this wave's loads of K of the next tile and of V of the
+      // current one have landed (`newer` loads may stay in flight: 6 = V of the
+      // next tile and both halves of the one after it), and V rows of tile t
+      // past kv_len are zeroed.
+      auto dma_wait = [&](int t, int vst, int newer) {
+        if (newer == 6)
+          asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        else if (newer == 2)
+          asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (t * KEYS + KEYS > kv_len) {
+#pragma unroll
+          for (int i = 2; i < 4; ++i) {
+            const int rp = 8 * (i & 1) + wave;
+            if (t * KEYS + 2 * rp + (lane >> 5) >= kv_len)
+              *(uint4*)(lds + VOFF + vst * VSZ + rp * 1024 + 16 * lane) = make_uint4(0, 0, 0, 0);
+          }
+        }
+      };
 
       // softmax state: the S-role's lazy running max (as prefill_kernel), the
       // O-role's row sums of the probabilities it accumulates
@@ -214,10 +276,15 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
       }
       const int t_mask = mask_from > 0 ? mask_from / KEYS : 0;
 
+      // swizzled K fragment offsets (direct-load rings): 32-dim slice s of key
+      // row 16*js + col sits at kbo[s & 3] + 256*(s >> 2) + 8192*js
+      uint32_t kbo[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) kbo[m] = col * 512 + 16 * (grp ^ (col & 3)) + 64 * (m ^ (col >> 2));
       // S-role: scores, softmax and probabilities of tile t (K in LDS stage
       // `stage`), published in the exchange buffers of parity t & 1.
       auto s_step = [&](int t, int stage) {
-        const uint8_t* sk = lds + stage * STAGE;
+        const uint8_t* sk = lds + stage * KSZ;
         f32x4 s[RGP][2];
 #pragma unroll
         for (int rg = 0; rg < RGP; ++rg)
@@ -233,7 +300,8 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
           for (int k = 0; k < KC; ++k)
 #pragma unroll
             for (int js = 0; js < 2; ++js)
-              a[k][js] = *(const uint4*)(sk + (16 * js + col) * RSK + (8 * grp + 32 * (KC * c + k)) * 2);
+              a[k][js] = DMA ? *(const uint4*)(sk + kbo[(KC * c + k) & 3] + 256 * ((KC * c + k) >> 2) + 8192 * js)
+                             : *(const uint4*)(sk + (16 * js + col) * RS + (8 * grp + 32 * (KC * c + k)) * 2);
         };
         kread(0, ka[0]);
 #pragma unroll
@@ -298,6 +366,14 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
           lds_alpha[t & 1][pr][rg][lane] = alpha[rg];
         }
       };
+      // swizzled V^T fragment offsets (direct-load rings): 32-byte segment jj of
+      // key row R sits at vbo[jj & 7] + 256*(jj >> 3)
+      uint32_t vbo[8];
+      {
+        const int R = 4 * grp + ((lane & 15) >> 2);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) vbo[m] = R * 512 + 8 * (lane & 3) + 32 * (m ^ (R & 7));
+      }
       // O-role: O^T += V^T.P^T of tile t (V in LDS stage `stage`), after the
       // rescale the S-role found for that tile.
       auto o_step = [&](int t, int stage) {
@@ -322,7 +398,8 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
 #pragma unroll
         for (int rg = 0; rg < RGP; ++rg)
           l_run[rg] = MT::sum2(pb[rg].w, MT::sum2(pb[rg].z, MT::sum2(pb[rg].y, MT::sum2(pb[rg].x, l_run[rg]))));
-        const uint8_t* vt0 = lds + stage * STAGE + KEYS * RSK + (4 * grp + ((lane & 15) >> 2)) * RSV + 8 * (lane & 3);
+        const uint8_t* vt = lds + VOFF + stage * VSZ;
+        const uint8_t* vt0 = vt + (4 * grp + ((lane & 15) >> 2)) * RS + 8 * (lane & 3);
         // V^T fragments in chunks of VC output tiles, one chunk read ahead of
         // the MFMAs that use it: the empty asm with a memory clobber keeps the
         // compiler from hoisting every read (64 registers) above the MFMAs.
@@ -332,8 +409,9 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
 #pragma unroll
           for (int k = 0; k < VC; ++k) {
             const int jj = VC * c + k;
-            const v4i16 x0 = ds_read_tr16(vt0 + 32 * jj);
-            const v4i16 x1 = ds_read_tr16(vt0 + 16 * RSV + 32 * jj);
+            const uint8_t* a0p = DMA ? vt + vbo[jj & 7] + 256 * (jj >> 3) : vt0 + 32 * jj;
+            const v4i16 x0 = ds_read_tr16(a0p);
+            const v4i16 x1 = ds_read_tr16(a0p + 16 * RS);
             const uint2 a0 = bitcast<uint2>(x0), a1 = bitcast<uint2>(x1);
             a[k] = make_uint4(a0.x, a0.y, a1.x, a1.y);
           }
@@ -351,52 +429,113 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
         }
       };
 
-      // ---- tile chunks, as prefill_kernel: step T stores tile T+1 into the
-      // stage tile T-2 used and loads tile T+1+NB; the S-role reads K of tile T,
-      // the O-role V of tile T-1.
-      for (c0 = 0; c0 * KEYS < kv_end; c0 += kPfTileCap) {
-        const int t0 = c0;
-        const int t1 = min(n_kt, c0 + kPfTileCap);
-        __syncthreads();
-        for (int e = tid; e < 2 * (t1 - t0); e += THREADS) {
-          const int key = min((t0 + (e >> 1)) * KEYS + 16 * (e & 1), key_cap);
-          const int pidx = (int)((unsigned)key / (unsigned)ps);
-          const int slot = key - pidx * ps;
-          lds_toff[e] = (int64_t)p.kv_indices[page_base + pidx] * page_bytes + (int64_t)slot * tok_bytes;
-        }
-        __syncthreads();
-        const int tl = t1 - 1;
-        const int n = t1 - t0;
+      // ---- tile chunks.  The S-role reads K of tile T, the O-role V of tile T-1.
+      if constexpr (DMA) {
+        // Step ii of a chunk: the S-role's scores of tile ii, the O-role's P.V
+        // of tile ii-1, then every wave's direct loads of tile ii+2 (ring stage
+        // (ii+2) % 4); before the barrier each wave's loads of K of tile ii+1
+        // and V of tile ii have landed (and are visible to all after it).
+        for (c0 = 0; c0 * KEYS < kv_end; c0 += CAP) {
+          const int t0 = c0;
+          const int t1 = min(n_kt, c0 + CAP);
+          __syncthreads();
+          for (int e = tid; e < 2 * (t1 - t0); e += THREADS) {
+            const int key = min((t0 + (e >> 1)) * KEYS + 16 * (e & 1), key_cap);
+            const int pidx = (int)((unsigned)key / (unsigned)ps);
+            const int slot = key - pidx * ps;
+            lds_toff[e] = (int64_t)p.kv_indices[page_base + pidx] * page_bytes + (int64_t)slot * tok_bytes;
+          }
+          __syncthreads();
+          const int tl = t1 - 1;
+          const int n = t1 - t0;
+          // the compiler's own loads (Q fragments, metadata) complete here, so
+          // it has no load of its own to wait for inside the step loop (a wait
+          // there would also drain the direct loads in flight)
+          __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+          dma_tile(t0, 0, 0);
+          dma_tile(min(t0 + 1, tl), 1, 1);
+          asm volatile("s_waitcnt vmcnt(6)" ::: "memory");  // K of tile t0
+          __syncthreads();
+          // step 0
+          if (n >= 3) dma_tile(t0 + 2, 2, 2);
+          if constexpr (S) s_step(t0, 0);
+          dma_wait(t0, 0, n >= 3 ? 6 : (n >= 2 ? 2 : 0));
+          __syncthreads();
+          // steps 1 .. n-3 (each loads tile ii+2): ring stage of tile ii = ii % 4 = (u + 1) % 4
+          for (int i = 1; i <= n - 3; i += 4) {
 #pragma unroll
-        for (int u = 0; u < NB; ++u) load_tile(min(t0 + u, tl), rr[u]);
-        store_tile(t0, rr[0], 0);
-        load_tile(min(t0 + NB, tl), rr[0]);
-        __syncthreads();
-        // step 0: scores of tile t0
-        if constexpr (S) s_step(t0, 0);
-        store_tile(min(t0 + 1, tl), rr[1 % NB], 1);
-        load_tile(min(t0 + 1 + NB, tl), rr[1 % NB]);
-        __syncthreads();
-        for (int i = 1; i < n; i += UNR) {
-#pragma unroll
-          for (int u = 0; u < UNR; ++u) {
-            const int ii = i + u;
-            if (ii >= n) break;
-            const int T = t0 + ii;
-            if constexpr (S) {
-              s_step(T, (u + 1) % 3);  // stage of tile T = ii % 3
-              store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
-              load_tile(min(T + 1 + NB, tl), rr[(u + 2) % NB]);
-            } else {
-              store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
-              load_tile(min(T + 1 + NB, tl), rr[(u + 2) % NB]);
-              o_step(T - 1, u % 3);  // stage of tile T-1 = (ii-1) % 3
+            for (int u = 0; u < 4; ++u) {
+              const int ii = i + u;
+              if (ii > n - 3) break;
+              const int T = t0 + ii;
+              if constexpr (S)
+                s_step(T, (u + 1) & 3);
+              else
+                o_step(T - 1, u);
+              dma_tile(T + 2, (u + 3) & 3, (u + 3) & 3);
+              dma_wait(T, (u + 1) & 3, 6);
+              __syncthreads();
             }
+          }
+          // the last two steps load nothing
+          for (int ii = max(1, n - 2); ii < n; ++ii) {
+            const int T = t0 + ii;
+            if constexpr (S)
+              s_step(T, ii & 3);
+            else
+              o_step(T - 1, (ii - 1) & 3);
+            dma_wait(T, ii & 3, T + 1 <= tl ? 2 : 0);
             __syncthreads();
           }
+          if constexpr (!S) o_step(tl, (n - 1) & 3);
         }
-        // last step: P.V of tile t1-1
-        if constexpr (!S) o_step(t1 - 1, (n - 1) % 3);
+      } else {
+        // as prefill_kernel: step T stores tile T+1 into the stage tile T-2 used
+        // and loads tile T+1+NB into registers
+        for (c0 = 0; c0 * KEYS < kv_end; c0 += kPfTileCap) {
+          const int t0 = c0;
+          const int t1 = min(n_kt, c0 + kPfTileCap);
+          __syncthreads();
+          for (int e = tid; e < 2 * (t1 - t0); e += THREADS) {
+            const int key = min((t0 + (e >> 1)) * KEYS + 16 * (e & 1), key_cap);
+            const int pidx = (int)((unsigned)key / (unsigned)ps);
+            const int slot = key - pidx * ps;
+            lds_toff[e] = (int64_t)p.kv_indices[page_base + pidx] * page_bytes + (int64_t)slot * tok_bytes;
+          }
+          __syncthreads();
+          const int tl = t1 - 1;
+          const int n = t1 - t0;
+#pragma unroll
+          for (int u = 0; u < NB; ++u) load_tile(min(t0 + u, tl), rr[u]);
+          store_tile(t0, rr[0], 0);
+          load_tile(min(t0 + NB, tl), rr[0]);
+          __syncthreads();
+          // step 0: scores of tile t0
+          if constexpr (S) s_step(t0, 0);
+          store_tile(min(t0 + 1, tl), rr[1 % NB], 1);
+          load_tile(min(t0 + 1 + NB, tl), rr[1 % NB]);
+          __syncthreads();
+          for (int i = 1; i < n; i += UNR) {
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) {
+              const int ii = i + u;
+              if (ii >= n) break;
+              const int T = t0 + ii;
+              if constexpr (S) {
+                s_step(T, (u + 1) % 3);  // stage of tile T = ii % 3
+                store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
+                load_tile(min(T + 1 + NB, tl), rr[(u + 2) % NB]);
+              } else {
+                store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
+                load_tile(min(T + 1 + NB, tl), rr[(u + 2) % NB]);
+                o_step(T - 1, u % 3);  // stage of tile T-1 = (ii-1) % 3
+              }
+              __syncthreads();
+            }
+          }
+          // last step: P.V of tile t1-1
+          if constexpr (!S) o_step(t1 - 1, (n - 1) % 3);
+        }
       }
 
       // ---- epilogue: the S-role publishes its row sums, the O-role writes the rows
