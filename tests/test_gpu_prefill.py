@@ -348,6 +348,41 @@ def test_prefill_long_context_page_chunks(gpu, hq, hkv, d, causal):
     assert err < TOL
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_prefill_d256_chunk_remainders(gpu, causal):
+    """Head_dim 256 (tiles loaded straight into LDS, page offsets staged 512 tiles at a time):
+    contexts that leave 1, 2 and 3 tiles in their last chunk and a one-tile request, with NaN
+    in every last page's slots past kv_len, against fp32 attention on the GPU."""
+    hq, hkv, d, ps = 16, 2, 256, 16
+    kv_lens = [16385, 16424, 16470, 31]   # 513, 514, 515 and 1 tiles of 32 keys
+    new_lens = [37, 5, 64, 31]
+    qo, kv_indptr, kv_indices, last = custom_batch(kv_lens, ps, sum(-(-np.array(kv_lens) // ps)) + 8, 23,
+                                                   new_lens=new_lens)
+    pool = int(kv_indices.max()) + 1
+    log(f"d256 chunk remainders causal={causal}: kv={kv_lens} new={new_lens}")
+    cache = torch.empty(pool, 2, ps, hkv, d, dtype=torch.bfloat16, device=gpu)
+    cache.normal_(generator=torch.Generator(device=gpu).manual_seed(7))
+    g = torch.Generator().manual_seed(8)
+    ntok = int(qo[-1])
+    q = torch.randn(ntok, hq, d, generator=g).to(torch.bfloat16).to(gpu)
+    k = torch.randn(ntok, hkv, d, generator=g).to(torch.bfloat16).to(gpu)
+    v = torch.randn(ntok, hkv, d, generator=g).to(torch.bfloat16).to(gpu)
+    w = FlashInferPrefillWrapper(workspace(gpu, 512 << 20), hq, hkv, d, ps, device=gpu)
+    w.plan(torch.as_tensor(qo), torch.as_tensor(kv_indptr), torch.as_tensor(kv_indices), torch.as_tensor(last),
+           causal=causal)
+    w.set_kv_cache(cache, k, v)
+    for r in range(len(kv_lens)):  # after the append: slots past each request's last key
+        page = int(kv_indices[kv_indptr[r + 1] - 1])
+        cache[page, :, int(last[r]):] = float("nan")
+    out = w.run(q, cache)
+    ref = _torch_ref_gpu(q, cache, qo, kv_indptr, kv_indices, last, causal, hq, hkv)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    err = (out.float() - ref).abs().max().item()
+    log(f"  max_abs={err:.3e}")
+    assert err < TOL
+
+
 def test_prefill_plan_index_inputs(gpu):
     """plan() over int64, strided and device index tensors gives bit-identical
     outputs and appended pages to int32 contiguous CPU tensors."""
