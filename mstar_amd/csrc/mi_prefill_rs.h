@@ -229,6 +229,11 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
         }
       }
       const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+      // The load's LDS address is M0 (one s_nop after writing it, as the ISA
+      // requires before an LDS-DMA load).  hipcc warns that m0 is a reserved
+      // register on the clobber list: the compiler emits no M0 use of its own
+      // in this kernel (no LDS-DMA builtin, s_sendmsg, movrel or interpolation),
+      // so nothing of its lives in M0 across these statements.
       auto dma_tile = [&](int t, int kst, int vst) {
         // both 16-row groups' page offsets first, then the four loads (scalar
         // base + 32-bit lane offset)
