@@ -342,27 +342,36 @@ WORKLOADS = {
 }
 
 
-def hbm_read_ceiling(buf: torch.Tensor, steps: int = 10) -> dict:
+def hbm_read_ceiling(buf: torch.Tensor, steps: int = 10, nbytes: int | None = None) -> dict:
     """The box's plain read rate over ``buf`` (the KV pool layer the decode
     kernel streams): ``mi_hbm_read`` with the decode kernel's 16-byte
-    non-temporal loads, median of ``steps`` launches timed with HIP events."""
+    non-temporal loads, median of ``steps`` launches timed with HIP events.
+    With ``nbytes`` (a job's size), each launch reads that many bytes, in turn
+    from up to three disjoint regions of ``buf``, as the decode bench cycles
+    pool layers, so a small job's ceiling is not served from the 256 MB
+    Infinity Cache and carries the same launch ramp and tail."""
     dev = buf.device
-    nbytes = buf.numel() * buf.element_size() // 16 * 16
+    total = buf.numel() * buf.element_size() // 16 * 16
+    size = total if nbytes is None else min(int(nbytes) // 16 * 16, total)
+    regions = max(1, min(3, total // size))
     grid = 8 * torch.cuda.get_device_properties(dev).multi_processor_count
     sink = torch.empty(4 * grid, dtype=torch.int32, device=dev)
     stream = _lib.stream_ptr(dev)
-    launch = lambda: _lib.check(_lib.lib().mi_hbm_read(buf.data_ptr(), nbytes, sink.data_ptr(), grid, stream),
-                                "mi_hbm_read")
-    launch()
+    launch = lambda i: _lib.check(_lib.lib().mi_hbm_read(buf.data_ptr() + (i % regions) * size, size, sink.data_ptr(),
+                                                         grid, stream), "mi_hbm_read")
+    for i in range(regions):
+        launch(i)
     evs = _kernel_events(steps, 2)
-    for e0, e1 in evs:
+    for i, (e0, e1) in enumerate(evs):
         e0.record()
-        launch()
+        launch(i)
         e1.record()
     torch.cuda.synchronize()
     us = float(np.median([e0.elapsed_time(e1) for e0, e1 in evs])) * 1e3
-    return {"kernel": "hbm_read_kernel", "what": "plain 16-byte non-temporal read of the KV pool layer",
-            "bytes": nbytes, "us_median": us, "GBps": nbytes / (us * 1e-6) / 1e9}
+    what = ("plain 16-byte non-temporal read of the KV pool layer" if nbytes is None else
+            f"plain 16-byte non-temporal read of the job's size, {regions} region(s) of the pool layer in turn")
+    return {"kernel": "hbm_read_kernel", "what": what, "bytes": size, "regions": regions, "us_median": us,
+            "GBps": size / (us * 1e-6) / 1e9}
 
 
 def _kernel_events(n: int, k: int):
@@ -408,6 +417,7 @@ def bench_decode(args, dev) -> dict:
     achieved = graph_bytes / (dec_us * 1e-6) / 1e9
     kv_tokens = int(seq_now.sum())
     ceiling = hbm_read_ceiling(kv[0])
+    ceiling_job = hbm_read_ceiling(kv[0], nbytes=graph_bytes)
     lo, hi = s.ctx[1], s.ctx[2]
     traffic, traffic_alg = measured_traffic(s.name)
     res = {
@@ -450,6 +460,8 @@ def bench_decode(args, dev) -> dict:
             "algorithmic_bytes_step_loop_mean": int(np.mean(bytes_per)),
             "hbm_read_ceiling": ceiling,
             "frac_of_read_ceiling": achieved / ceiling["GBps"],
+            "hbm_read_same_bytes": ceiling_job,
+            "frac_of_same_bytes_read": ceiling_job["us_median"] / dec_us,
         },
     }
     pos_now = seq_now
@@ -975,6 +987,8 @@ def side_configs(args, dev) -> dict:
                 "kernel": rf["kernel"], "kernel_us": rf["kernel_us"], "decode_plus_merge_us": rf["decode_plus_merge_us"],
                 "algorithmic_bytes": rf["algorithmic_bytes"], "GBps": rf["achieved"], "hbm_frac": rf["frac"],
                 "read_ceiling_GBps": rf["hbm_read_ceiling"]["GBps"], "frac_of_read_ceiling": rf["frac_of_read_ceiling"],
+                "same_bytes_read_us": rf["hbm_read_same_bytes"]["us_median"],
+                "frac_of_same_bytes_read": rf["frac_of_same_bytes_read"],
             }
         _log(f"{name}: " + json.dumps({k: v for k, v in out[name].items() if k != "workload"}))
     return out
