@@ -79,7 +79,6 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   __shared__ int64_t lds_toff[2 * kPfTileCap];
 
   __shared__ int s_unit;
-  const int nkv = p.num_kv_heads;
   const int n_tiles = p.hdr[0];
   const int xcd = (int)blockIdx.x & 7;  // workgroups are dispatched to the 8 XCDs round-robin
 
@@ -188,7 +187,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
 #pragma unroll
     for (int i = 0; i < NL; ++i) pg[i] = lds_toff[2 * (t - c0) + (l_grp[i] >> 4)];
   };
-  auto load_tile_at = [&](int t, const int64_t (&pg)[NL], uint4 (&r)[NL]) {
+  auto load_tile_at = [&](const int64_t (&pg)[NL], uint4 (&r)[NL]) {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       if (2 * HALF % THREADS == 0 || tid + i * THREADS < 2 * HALF) {
@@ -200,7 +199,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
   auto load_tile = [&](int t, uint4 (&r)[NL]) {
     int64_t pg[NL];
     tile_pages(t, pg);
-    load_tile_at(t, pg, r);
+    load_tile_at(pg, r);
   };
   // TAIL: the tile may reach past kv_len (only the request's last tile can),
   // so its V rows past the end are overwritten with zeros
@@ -454,7 +453,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
           store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
           sm_max(T - 1, sc);
           sm_exp(sc, pbk);
-          load_tile_at(min(T + 1 + NB, tl), pg4, rr[(u + 2) % NB]);
+          load_tile_at(pg4, rr[(u + 2) % NB]);
           __builtin_amdgcn_s_setprio(0);
         }
         // scores of tile T first (group B's softmax waits on them), then P.V of
@@ -465,7 +464,7 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
         if (!grp_a) {
           __builtin_amdgcn_s_setprio(1);
           store_tile(min(T + 1, tl), rr[(u + 2) % NB], (u + 2) % 3);
-          load_tile_at(min(T + 1 + NB, tl), pg4, rr[(u + 2) % NB]);
+          load_tile_at(pg4, rr[(u + 2) % NB]);
           sm_max(T, sc);
           sm_exp(sc, pbk);
           __builtin_amdgcn_s_setprio(0);

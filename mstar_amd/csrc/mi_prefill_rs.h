@@ -37,7 +37,7 @@ __global__ __launch_bounds__(512) void prefill_rs_kernel(PrefillParams p) {
   constexpr int RGP = D > 128 ? 2 : 4, PROWS = 16 * RGP;
   static_assert(C::ROWS == 4 * PROWS, "tile rows = four pairs");
   constexpr int KS = D / 32, VW = D / 16, KEYS = C::KEYS, RSK = C::RSK, RSV = C::RSV, ESZ = C::ESZ, CPR = C::CPR;
-  constexpr int THREADS = C::THREADS, NL = C::NL, HALF = C::HALF, STAGE = C::STAGE;
+  constexpr int THREADS = C::THREADS, NL = C::NL, HALF = C::HALF;
   constexpr int LCH = FP8 ? 32 : 16;  // LDS bytes per loaded chunk
   constexpr float kNegInf = -__builtin_inff();
   static_assert(THREADS == 512, "four wavefront pairs");
