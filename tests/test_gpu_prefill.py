@@ -348,6 +348,33 @@ def test_prefill_long_context_page_chunks(gpu, hq, hkv, d, causal):
     assert err < TOL
 
 
+def test_prefill_head_dim_256_full_batch(gpu):
+    """The head_dim 256 batch the bench times, at full size: 8 requests of 2048 new
+    tokens over 4096..7680-token contexts, 16 q / 2 kv heads, page 16, causal, pages
+    in a random order, against fp32 attention on the GPU."""
+    hq, hkv, d, ps = 16, 2, 256, 16
+    kv_lens = [4096 + 512 * i for i in range(8)]
+    new = [2048] * 8
+    pages = [-(-n // ps) for n in kv_lens]
+    pool = sum(pages) + 8
+    kv_indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int32)
+    kv_indices = np.random.default_rng(0).permutation(pool)[: kv_indptr[-1]].astype(np.int32)
+    last = np.array([n - (p - 1) * ps for n, p in zip(kv_lens, pages)], np.int32)
+    qo = np.concatenate([[0], np.cumsum(new)]).astype(np.int32)
+    log(f"head_dim 256 full batch: kv={kv_lens} new={new}")
+    g = torch.Generator(device=gpu).manual_seed(5)
+    cache = torch.randn(pool, 2, ps, hkv, d, device=gpu, generator=g).to(torch.bfloat16)
+    q = torch.randn(int(qo[-1]), hq, d, device=gpu, generator=g).to(torch.bfloat16)
+    w = FlashInferPrefillWrapper(workspace(gpu, 512 << 20), hq, hkv, d, ps, device=gpu)
+    w.plan(*(torch.from_numpy(a) for a in (qo, kv_indptr, kv_indices, last)), causal=True)
+    out = w.run(q, cache)
+    ref = _torch_ref_gpu(q, cache, qo, kv_indptr, kv_indices, last, True, hq, hkv)
+    torch.cuda.synchronize()
+    err = (out.float() - ref).abs().max().item()
+    log(f"  max_abs={err:.3e}")
+    assert err < TOL
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_prefill_d256_chunk_remainders(gpu, causal):
     """Head_dim 256 (tiles loaded straight into LDS, page offsets staged 512 tiles at a time):
