@@ -449,6 +449,7 @@ def bench_decode(args, dev) -> dict:
             "traffic_source": (f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes over the {s.name} bench, scaled by a "
                                f"1 GiB copy; per decode launch of a plan with {traffic_alg} algorithmic bytes"
                                if traffic is not None else None),
+            "traffic_per_algorithmic_byte": traffic / traffic_alg if traffic and traffic_alg else None,
             "kernel": "decode_kernel",
             "kernel_us": dec_us,
             "kernel_us_how": (f"HIP graph replay of {-(-12 // layers) * layers} decode launches of the last step's plan "
@@ -930,7 +931,7 @@ def bench_prefill_d256(dev, steps: int) -> dict:
     torch.cuda.synchronize()
     us = float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3
     flops = sum(4 * hq * d * (kl - n + t + 1) for kl, n in zip(kv_lens, new) for t in range(n))
-    return {"kernel": "prefill_rs_kernel<BF16, false>", "us": us, "algorithmic_flops": flops,
+    return {"kernel": "prefill_rs_kernel<BF16, false, 256>", "us": us, "algorithmic_flops": flops,
             "TFLOPs": flops / us / 1e6, "frac": flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS}
 
 
