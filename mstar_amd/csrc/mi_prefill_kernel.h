@@ -291,9 +291,10 @@ __global__ __launch_bounds__(64 * pf_waves(D)) void prefill_kernel(PrefillParams
       for (int js = 0; js < 2; ++js)
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg) s[rg][js] = MT::mma_16x16x32(a[js][st], qf[rg][st], s[rg][js]);
-    // K fragment reads one slice ahead of the MFMAs that use them (four MFMAs
-    // per slice cover the LDS latency; c4 592 -> 586 us against all reads first).
-    constexpr int KLA = 1;
+    // K fragment reads KLA slices ahead of the MFMAs that use them: at head_dim
+    // 128 three of the four (c4 tiles 534-561 -> 522-554 us against one slice
+    // ahead, 550-556 with all four first), at head_dim 64 one of the two.
+    constexpr int KLA = KS >= 4 ? 3 : 1;
     __builtin_amdgcn_sched_group_barrier(0x100, 2 * KLA, 0);
 #pragma unroll
     for (int st = KLA; st < KS; ++st) {
